@@ -1,0 +1,309 @@
+"""Benchmark of the int4 routed-expert MoE layer on one MI355X.
+
+Headline workload: one Mixtral-8x7B-shape MoE layer decode, M = 1 token:
+router GEMV + softmax top-2 on the device, then the fused int4 expert FFN
+(gate/up/SiLU, down, weighted combine) over the 2 routed experts; 8 experts
+of hidden 4096 / inter 14336, int4 g128, fp16 scales, all resident in HBM.
+One step = one MoE layer on one fixed synthetic token; `value` is the mean
+microseconds per layer over the timed steps (lower is better).
+
+Also reported (same JSON line, "extra"): Mixtral M=4 and DeepSeek-V3-shape
+decode (256 routed experts + 1 shared, inter 2048, hidden 7168, sigmoid
+top-8) for M = 1, 2, 4, each with its dominant-kernel roofline.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E peak
+EV_ROUTE, EV_PREP, EV_GATEUP, EV_DOWN, EV_KINDS = 0, 1, 2, 3, 6
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Layer:
+    """Device state of one MoE layer workload.
+
+    To measure weights streamed from HBM rather than from the 256 MB
+    Infinity Cache, steps rotate over `n_sets` independent expert sets (each
+    a full layer of resident experts) and a pool of `n_pool` different input
+    tokens (so routing, and with it the touched experts, changes per step).
+    """
+
+    def __init__(self, shape, M, seed, n_sets=1, n_pool=16):
+        from wisp_amd import moe, synth
+        from wisp_amd.hip import DeviceBuffer, Stream, to_device
+        self.shape, self.M, self.n_pool = shape, M, n_pool
+        rng = np.random.default_rng(seed)
+        t0 = time.time()
+        keep = range(shape.n_experts) if shape.n_experts <= 8 else ()
+        self.arenas = []
+        for si in range(n_sets):
+            self.arenas.append(moe.ExpertArena(
+                shape.n_experts, shape.inter, shape.hidden, shape.group_size,
+                lambda e, out, si=si: synth.make_blob(np.random.default_rng([seed, si, e]),
+                                                      shape.inter, shape.hidden, shape.group_size,
+                                                      expert=e, out=out),
+                has_zeros=False, keep_host=keep if si == 0 else ()))
+        self.shared_blob = None
+        self.shared_dev = None
+        if shape.shared:
+            self.shared_blob = synth.make_blob(np.random.default_rng([seed, 99999]), shape.inter,
+                                               shape.hidden, shape.group_size, expert=99999)
+            self.shared_dev = DeviceBuffer(self.shared_blob.nbytes + 16)
+            self.shared_dev.upload(self.shared_blob, offset=8)
+        log(f"{shape.name} M={M}: {n_sets} expert set(s) resident in {time.time() - t0:.1f}s")
+        self.W = synth.make_router(rng, shape.n_experts, shape.hidden)
+        self.dW = to_device(self.W)
+        self.kind = moe.ROUTER_SOFTMAX if shape.router == "softmax" else moe.ROUTER_SIGMOID
+        self.stream = Stream()
+        self.set_tokens(M, rng)
+
+    def set_tokens(self, M, rng):
+        from wisp_amd import moe, synth
+        from wisp_amd.hip import DeviceBuffer, to_device
+        s = self.shape
+        self.M = M
+        self.x = synth.make_x(rng, self.n_pool * M, s.hidden).reshape(self.n_pool, M, s.hidden)
+        self.dx = to_device(self.x)
+        self.logits = DeviceBuffer(4 * M * s.n_experts)
+        self.idx = DeviceBuffer(4 * M * s.top_k)
+        self.w = DeviceBuffer(4 * M * s.top_k)
+        self.ws = DeviceBuffer(moe.decode_workspace_bytes(self.arenas[0].layout, M, s.top_k, s.shared))
+        self.out16 = DeviceBuffer(2 * M * s.hidden)
+        self.out32 = DeviceBuffer(4 * M * s.hidden)
+        self._bytes = None
+
+    def xptr(self, i):
+        return self.dx.ptr + (i % self.n_pool) * self.M * self.shape.hidden * 2
+
+    def step(self, i):
+        from wisp_amd import moe
+        s = self.shape
+        a = self.arenas[i % len(self.arenas)]
+        moe.moe_route(self.dW.ptr, 0, self.xptr(i), self.M, s.hidden, s.n_experts, s.top_k,
+                      self.kind, self.logits.ptr, self.idx.ptr, self.w.ptr, self.stream.handle)
+        moe.moe_decode_int4(a.table.ptr, self.shared_dev.ptr + 8 if s.shared else 0, a.layout,
+                            self.xptr(i), self.M, self.idx.ptr, self.w.ptr, s.top_k, s.n_experts,
+                            self.ws, self.out32.ptr, self.out16.ptr, self.stream.handle)
+
+    def token_bytes(self):
+        """Per pool token: algorithmic HBM bytes (packed + scales; zeros are
+        +0 and not read) of the gate/up kernel, the down kernel, the router
+        and the layer, from the routing the device produces for it."""
+        from wisp_amd.hip import synchronize
+        if self._bytes is None:
+            s = self.shape
+            mat = (s.inter * s.hidden) // 2 + 2 * (s.inter * s.hidden // s.group_size)
+            router = s.n_experts * s.hidden * 2
+            out = []
+            for t in range(self.n_pool):
+                self.step(t)
+                synchronize()
+                ids = self.idx.download(np.int32, (self.M, s.top_k))
+                n_u = len({int(e) for e in ids.reshape(-1)}) + (1 if s.shared else 0)
+                out.append({"n_unique": n_u, "gate_up": 2 * n_u * mat, "down": n_u * mat,
+                            "router": router, "layer": 3 * n_u * mat + router})
+            self._bytes = out
+        return self._bytes
+
+    def mean_bytes(self, steps):
+        tb = self.token_bytes()
+        keys = tb[0].keys()
+        return {k: float(np.mean([tb[i % self.n_pool][k] for i in range(steps)])) for k in keys}
+
+
+def time_layer(layer, steps, warmup):
+    from wisp_amd import _lib
+    from wisp_amd.hip import Event, synchronize
+    for i in range(warmup):
+        layer.step(i)
+    synchronize()
+    e0, e1 = Event(), Event()
+    t0 = time.perf_counter()
+    e0.record(layer.stream.handle)
+    for i in range(steps):
+        layer.step(i)
+    e1.record(layer.stream.handle)
+    synchronize()
+    host_ms = (time.perf_counter() - t0) * 1e3
+    dev_ms = e0.elapsed_ms(e1)
+    # per-kernel durations: same steps again with events around each kernel
+    evs = [[Event() for _ in range(2 * EV_KINDS)] for _ in range(steps)]
+    arrs = [(ctypes.c_void_p * (2 * EV_KINDS))(*[e.handle for e in row]) for row in evs]
+    lib = _lib.lib()
+    for i in range(steps):
+        lib.wisp_amd_set_kernel_events(ctypes.cast(arrs[i], ctypes.c_void_p), EV_KINDS)
+        layer.step(i)
+    lib.wisp_amd_set_kernel_events(None, 0)
+    synchronize()
+    kern = {}
+    for name, k in (("route", EV_ROUTE), ("prep", EV_PREP), ("gate_up", EV_GATEUP), ("down", EV_DOWN)):
+        kern[name] = 1e3 * float(np.mean([evs[i][2 * k].elapsed_ms(evs[i][2 * k + 1]) for i in range(steps)]))
+    return {"us_per_layer": 1e3 * dev_ms / steps, "host_us_per_layer": 1e3 * host_ms / steps,
+            "kernel_us": kern}
+
+
+def cpu_baseline(layer, budget_s=10.0):
+    """The oracle's vectorised CPU path (AVX-512 or AVX2, OpenMP over rows)
+    on this host: router + top-k + the routed experts' FFN, one token per
+    layer, cycling over the same token pool as the GPU steps."""
+    from oracle import oracle as O
+    s = layer.shape
+    blobs = layer.arenas[0].host
+
+    def one(i):
+        x = layer.x[i % layer.n_pool, 0].astype(np.float32)
+        idx, w, _ = O.router_topk(layer.W.view(np.uint16), None, x, s.top_k, kind=s.router)
+        acc = np.zeros(s.hidden, np.float32)
+        if layer.shared_blob is not None:
+            O.expert_ffn(layer.shared_blob, x, acc, 1.0, fast=True)
+        for e, we in zip(idx, w):
+            O.expert_ffn(blobs[int(e)], x, acc, float(we), fast=True)
+        return acc
+
+    one(0)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while (time.perf_counter() < t_end and len(times) < 2000) or len(times) < 3:
+        t0 = time.perf_counter()
+        one(len(times))
+        times.append(time.perf_counter() - t0)
+    isa = {2: "avx512", 1: "avx2", 0: "scalar"}[O.orc().orc_fast_isa()]
+    return {"value": round(1e6 * float(np.median(times)), 1), "unit": "us/layer",
+            "cores": int(O.orc().orc_num_threads()), "kind": "port",
+            "sample": f"{len(times)} {s.name} M=1 layers (router + top-{s.top_k} experts), median; "
+                      f"{isa} OpenMP fp32 path of oracle/wisp_oracle.c",
+            "cpu": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def roofline(nbytes, us):
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def load_traffic(workload):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(workload)
+    except (OSError, ValueError):
+        return None
+
+
+def measure(layer, steps, warmup):
+    r = time_layer(layer, steps, warmup)
+    b = layer.mean_bytes(steps)
+    us = r["us_per_layer"]
+    return {
+        "us_per_layer": round(us, 3),
+        "layer_hbm_frac": round(b["layer"] / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "n_unique_experts": round(b["n_unique"], 2),
+        "kernel_us": {k: round(v, 3) for k, v in r["kernel_us"].items()},
+        "gate_up": {**roofline(b["gate_up"], r["kernel_us"]["gate_up"]),
+                    "bytes_per_launch": int(b["gate_up"])},
+        "down": {**roofline(b["down"], r["kernel_us"]["down"]), "bytes_per_launch": int(b["down"])},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--quick", action="store_true", help="headline workload only")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the int4 MoE expert path here is a single-GPU "
+              "build (expert-parallel sharding is described in DESIGN.md, not run)", file=sys.stderr)
+        sys.exit(2)
+
+    from wisp_amd import synth
+    from wisp_amd.hip import device_count
+    if device_count() < 1:
+        print("no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+
+    # 4 Mixtral expert sets (3 GB) so consecutive steps stream cold weights
+    head = Layer(synth.MIXTRAL, 1, seed=1234, n_sets=4)
+    m = measure(head, args.steps, args.warmup)
+    log(f"mixtral M=1: {m['us_per_layer']:.2f} us/layer, kernels {m['kernel_us']}")
+    gu = dict(m["gate_up"])
+    gu["traffic"] = load_traffic("mixtral-decode-m1/gate_up")
+    result = {
+        "metric": "us per MoE layer, int4 expert decode (Mixtral-8x7B shape, M=1)",
+        "value": m["us_per_layer"],
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(m["us_per_layer"] / 1e3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": "mixtral-8x7b-moe-decode-m1", "hidden": 4096, "inter": 14336,
+                   "experts": 8, "top_k": 2, "tokens": 1, "weights": "int4 g128 fp16 scales",
+                   "router": "softmax top-2 on device", "expert_sets_rotated": 4,
+                   "parallelism": "single-gpu"},
+        "layer_hbm_frac": m["layer_hbm_frac"],
+        "kernel_us": m["kernel_us"],
+        "roofline": {"bound": gu["bound"], "achieved": gu["achieved"], "peak": gu["peak"],
+                     "unit": gu["unit"], "frac": gu["frac"], "traffic": gu["traffic"],
+                     "kernel": "moe gate_up (fused int4 gate+up+SiLU)",
+                     "bytes_per_launch": gu["bytes_per_launch"]},
+        "down_roofline": m["down"],
+    }
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(head)
+        log(f"cpu baseline {result['cpu_baseline']['value']:.0f} us/layer")
+
+    if not args.quick:
+        extra = {}
+        rng = np.random.default_rng(99)
+        head.set_tokens(4, rng)
+        extra["mixtral-8x7b-decode-m4"] = measure(head, max(20, args.steps // 2), 5)
+        log(f"mixtral M=4: {extra['mixtral-8x7b-decode-m4']}")
+        del head
+        ds = Layer(synth.DSV3, 1, seed=777, n_sets=1)
+        for M in (1, 2, 4):
+            if M > 1:
+                ds.set_tokens(M, rng)
+            key = f"deepseek-v3-decode-m{M}"
+            extra[key] = measure(ds, max(20, args.steps // 2), 5)
+            log(f"{key}: {extra[key]}")
+        result["extra"] = extra
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,246 @@
+/*
+ * wisp_amd.h — C-ABI of the MI355X (gfx950) int4 routed-expert MoE path.
+ *
+ * Plain extern "C" functions over device pointers, sizes and HIP streams;
+ * all device buffers are caller-owned unless stated. Every launcher is
+ * stream-ordered and host-non-blocking unless stated.
+ *
+ * Section 1 keeps the reference engine's kernel-launcher names, argument
+ * order and error behaviour (csrc/core/wisp_engine.h:496-583, the expert
+ * path subset) with HIP types in place of the CUDA ones, so the reference's
+ * gpu_expert_ffn call shape (csrc/core/wisp_engine.c:1507-1531) links
+ * unchanged. The later sections are new launchers for what the reference
+ * does not have: device-side routing, the expert-offset builder,
+ * gather/scatter, a fused int4 decode for M = 1..4 tokens and the prefill
+ * grouped GEMM.
+ *
+ * Quant format (csrc/cuda/expert_loader.cu:8-13): two int4 values per byte,
+ * low nibble = even flat index; groups of group_size consecutive elements of
+ * the row-major matrix share one fp16 scale and one fp16 zero;
+ * value = (nibble - 8) * scale + zero.
+ */
+#ifndef WISP_AMD_H
+#define WISP_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifndef __HIP_PLATFORM_AMD__
+#define __HIP_PLATFORM_AMD__ 1
+#endif
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Raw fp16 bits; same size/layout as the reference's wisp_half
+ * (csrc/core/wisp_engine.h:32-40). */
+typedef uint16_t wisp_half;
+
+/* ======================================================================= *
+ * 1. Reference launcher interface (hot-path subset)
+ * ======================================================================= */
+
+/* out[i] = fp16((nib_i - 8) * s[i/gs] + z[i/gs]) for i < n_elements.
+ * Returns hipErrorInvalidValue for n_elements <= 0 or group_size <= 0,
+ * else the launch status. Replaces csrc/cuda/expert_loader.cu:46-63
+ * (declared at csrc/core/wisp_engine.h:545-550). */
+hipError_t launch_dequant_expert(const uint8_t* d_packed,
+                                 const wisp_half* d_scales,
+                                 const wisp_half* d_zeros,
+                                 wisp_half* d_output,
+                                 int n_elements, int group_size,
+                                 hipStream_t stream);
+
+/* Three H2D copies (packed, scales, zeros) into the tmp buffers on `stream`,
+ * then launch_dequant_expert into d_output. Replaces
+ * csrc/cuda/expert_loader.cu:67-97 (csrc/core/wisp_engine.h:551-559). */
+hipError_t async_load_expert(const uint8_t* h_packed,
+                             const wisp_half* h_scales,
+                             const wisp_half* h_zeros,
+                             uint8_t* d_packed_tmp,
+                             wisp_half* d_scales_tmp,
+                             wisp_half* d_zeros_tmp,
+                             wisp_half* d_output,
+                             int n_elements, int group_size,
+                             hipStream_t stream);
+
+/* y[r] = sum_c W[r,c] * x[c]; fp16 W, fp32 x/y/accumulate. Early-returns
+ * on rows <= 0 or cols <= 0. Replaces csrc/cuda/matmul.cu:43-65
+ * (csrc/core/wisp_engine.h:499-500). */
+void wisp_gpu_gemv_f16(const wisp_half* W, const float* x, float* y,
+                       int rows, int cols, hipStream_t s);
+
+/* h[r] = silu(Wg[r].x) * (Wu[r].x); fp16 W, fp32 x/h. Early-returns on
+ * inter <= 0 or cols <= 0. Replaces csrc/cuda/matmul.cu:163-205
+ * (csrc/core/wisp_engine.h:509-511). */
+void wisp_gpu_swiglu_ffn(const wisp_half* Wg, const wisp_half* Wu,
+                         const float* x, float* h, int inter, int cols,
+                         hipStream_t s);
+
+/* acc[i] += w * x[i]. Early-returns on n <= 0. Replaces
+ * csrc/cuda/matmul.cu:150-161 (csrc/core/wisp_engine.h:512-513). */
+void wisp_gpu_scale_accum(float* acc, const float* x, float w, int n,
+                          hipStream_t s);
+
+/* logits = W x + bias (fp16 W/bias, fp32 x), softmax, top-k (ties to the
+ * lowest index), renormalised weights. out_idx/out_w are HOST pointers
+ * (pinned for true asynchrony) filled by async D2H on `s`; the caller
+ * synchronises `s` before reading them. top_k is clamped to 64; returns
+ * early on n_experts <= 0 or top_k <= 0. The selection is staged in a
+ * file-scope device array per device (no allocation). Replaces
+ * csrc/cuda/router.cu:140-171 (csrc/core/wisp_engine.h:534-537). */
+void wisp_gpu_router_topk(const wisp_half* W, const wisp_half* bias,
+                          const float* x, float* logits_scratch,
+                          int n_experts, int hidden, int top_k,
+                          int* out_idx, float* out_w, hipStream_t s);
+
+/* ======================================================================= *
+ * 2. Expert blob layout
+ *    Blob = 120 B header (csrc/core/wisp_engine.h:214-238) then, for gate,
+ *    up, down in order, [packed][scales][zeros].
+ * ======================================================================= */
+
+typedef struct {
+    uint64_t packed_off[3];   /* byte offsets from the blob base            */
+    uint64_t scales_off[3];
+    uint64_t zeros_off[3];
+    uint32_t rows[3];         /* gate [inter,hidden], up [inter,hidden],    */
+    uint32_t cols[3];         /* down [hidden,inter]                        */
+    uint32_t group_size;
+    uint32_t has_zeros;       /* 0: zeros are all +0 and are not read       */
+    uint64_t total_bytes;     /* header + all sections                      */
+} WispExpertLayout;
+
+/* Parse a blob header held in HOST memory (same checks as
+ * csrc/core/wisp_engine.c:268-303). Sets has_zeros = 1. Returns 0, or
+ * -1 too small / -2 bad magic, version or n_mats / -3 truncated. */
+int wisp_expert_layout_from_blob(const void* host_blob, size_t blob_size,
+                                 WispExpertLayout* out);
+
+/* 0 if the fused int4 kernels accept this layout with blobs at the given
+ * device address alignment: all sections 16-byte aligned for blob bases at
+ * 8 mod 16 (the tier's slot placement), gate/up [inter, hidden], down
+ * [hidden, inter], hidden and inter multiples of 128, group_size in
+ * {32, 64} or a multiple of 128 dividing both. Else hipErrorInvalidValue. */
+hipError_t wisp_expert_layout_check(const WispExpertLayout* L);
+
+/* ======================================================================= *
+ * 3. Routing (device-resident) and the expert-offset builder
+ * ======================================================================= */
+
+enum { WISP_ROUTER_SOFTMAX = 0, WISP_ROUTER_SIGMOID = 1 };
+
+/* For each of n_tokens rows of x (fp16 [n_tokens, hidden]):
+ *   logits = W x (+ bias for softmax, fp32 accumulate), then
+ *   SOFTMAX: p = softmax(logits); top-k of p; w = p_k / sum p_k
+ *            (csrc/core/wisp_engine.c:782-818)
+ *   SIGMOID: s = sigmoid(logits); top-k of s (+ bias if given);
+ *            w = s_k / sum s_k (no reference counterpart)
+ * Ties go to the lowest expert index. Writes d_logits [n_tokens, n_experts]
+ * (the post-activation scores), d_topk_idx / d_topk_w [n_tokens, top_k].
+ * n_experts <= 1024, top_k <= 64, hidden % 8 == 0. */
+hipError_t wisp_gpu_moe_route(const wisp_half* d_router_w,
+                              const wisp_half* d_bias, const wisp_half* d_x,
+                              int n_tokens, int hidden, int n_experts,
+                              int top_k, int kind, float* d_logits,
+                              int* d_topk_idx, float* d_topk_w,
+                              hipStream_t s);
+
+/* Top-k selection and weights only, from given raw logits
+ * [n_tokens, n_experts] (fp32), with the same rules as wisp_gpu_moe_route.
+ * d_scores receives the post-activation scores. */
+hipError_t wisp_gpu_topk_from_logits(const float* d_logits,
+                                     const wisp_half* d_bias, int n_tokens,
+                                     int n_experts, int top_k, int kind,
+                                     float* d_scores, int* d_topk_idx,
+                                     float* d_topk_w, hipStream_t s);
+
+/* Expert-offset builder over the n_tokens*top_k (token, slot) pairs:
+ * counts[e]; offsets = exclusive scan, n_experts+1 entries; order[] lists
+ * flat pair indices (token*top_k + slot) grouped by expert, stable in flat
+ * order within an expert; inv[flat] = position of that pair in order[]
+ * (-1 for pairs with an out-of-range expert id). One workgroup;
+ * n_experts <= 4096. */
+hipError_t wisp_gpu_expert_offsets(const int* d_topk_idx, int n_tokens,
+                                   int top_k, int n_experts, int* d_counts,
+                                   int* d_offsets, int* d_order, int* d_inv,
+                                   hipStream_t s);
+
+/* Gather: xg[p, :] = x[order[p] / top_k, :] for p < n_pairs (fp16). The
+ * first n_pairs entries of order must be valid pair indices of x's tokens
+ * (offsets[n_experts] of wisp_gpu_expert_offsets); negative entries are
+ * skipped. */
+hipError_t wisp_gpu_moe_gather(const wisp_half* d_x, const int* d_order,
+                               int n_pairs, int top_k, int hidden,
+                               wisp_half* d_xg, hipStream_t s);
+
+/* Weighted combine ("scatter-add" done as a per-token gather so it is
+ * deterministic): out[t, :] (+)= sum over slots k in order of
+ * w[t, k] * y[inv[t*top_k + k], :]; pairs with inv < 0 are skipped.
+ * y fp32 [n_pairs, hidden]; out fp32 [n_tokens, hidden]; accumulate != 0
+ * adds to out instead of overwriting. */
+hipError_t wisp_gpu_moe_scatter(const float* d_y, const int* d_inv,
+                                const float* d_topk_w, int n_tokens,
+                                int top_k, int hidden, int accumulate,
+                                float* d_out, hipStream_t s);
+
+/* ======================================================================= *
+ * 4. Fused int4 MoE decode, M = 1..4 tokens
+ *
+ *    out[t] = shared(x_t) + sum_k w[t,k] * expert_{idx[t,k]}(x_t)
+ *    expert(x) = down . (silu(gate . x) * (up . x))
+ *
+ *    Two kernels after a small prep kernel: (a) gate+up+SiLU over every
+ *    unique expert touched by the M tokens in one launch, (b) down
+ *    projection and weighted combine for all of them in one launch.
+ *    Weights stream from the blobs in place; nothing is dequantised to
+ *    memory. Routing stays on the device.
+ * ======================================================================= */
+
+enum { WISP_DTYPE_F16 = 0, WISP_DTYPE_F32 = 1 };
+
+/* Workspace bytes for wisp_gpu_moe_decode_int4. */
+size_t wisp_moe_decode_workspace_bytes(const WispExpertLayout* L,
+                                       int n_tokens, int top_k,
+                                       int has_shared);
+
+/* d_expert_table: device array [n_experts] of device blob base pointers
+ *   (each blob base at 8 mod 16, see wisp_expert_layout_check).
+ * d_shared_blob: device blob of the always-on shared expert, or NULL.
+ * d_x: [n_tokens, hidden], fp16 or fp32 per x_dtype.
+ * d_topk_idx / d_topk_w: [n_tokens, top_k] (device); idx < 0 is skipped.
+ * d_out_f32 / d_out_f16: [n_tokens, hidden]; either may be NULL. With
+ *   accumulate != 0, d_out_f32 is added to instead of overwritten.
+ * Returns hipErrorInvalidValue for n_tokens outside 1..4, a layout that
+ * wisp_expert_layout_check rejects, or a workspace that is too small. */
+hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table,
+                                    const void* d_shared_blob,
+                                    const WispExpertLayout* L,
+                                    const void* d_x, int x_dtype,
+                                    int n_tokens, const int* d_topk_idx,
+                                    const float* d_topk_w, int top_k,
+                                    int n_experts, void* d_workspace,
+                                    size_t workspace_bytes, int accumulate,
+                                    float* d_out_f32, wisp_half* d_out_f16,
+                                    hipStream_t s);
+
+/* ======================================================================= *
+ * 9. Profiling hook
+ * ======================================================================= */
+
+/* When events != NULL, the fused launchers record events[2*k] before and
+ * events[2*k+1] after each kernel of kind k < n_pairs on the launch stream:
+ * k = 0 router (wisp_gpu_moe_route), 1 decode prep, 2 decode gate/up,
+ * 3 decode down, 4 prefill gate/up, 5 prefill down. Process-wide; for
+ * timing runs only; not thread-safe. */
+void wisp_amd_set_kernel_events(hipEvent_t* events, int n_pairs);
+
+/* Library version string. */
+const char* wisp_amd_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WISP_AMD_H */

@@ -1,0 +1,37 @@
+"""Helpers for the GPU parity tests (imported by tests/test_gpu_*.py)."""
+import numpy as np
+
+from wisp_amd import synth
+from wisp_amd.hip import DeviceBuffer, to_device
+
+
+def expert_rng(seed, e):
+    return np.random.default_rng([seed, e])
+
+
+def make_expert(seed, e, inter, hidden, gs, zeros=False, out=None):
+    return synth.make_blob(expert_rng(seed, e), inter, hidden, gs, expert=e, zeros=zeros, out=out)
+
+
+def rel_err(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.max(np.abs(got - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+def cosine(got, want):
+    a = np.asarray(got, np.float64).ravel()
+    b = np.asarray(want, np.float64).ravel()
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-300))
+
+
+# Parity bar for fp16 outputs: max |err| / max |ref|
+# <= 1e-2 and cosine >= 0.9999 against the CPU oracle.
+MAX_REL = 1e-2
+MIN_COS = 0.9999
+
+
+def assert_close(got, want, what=""):
+    r, c = rel_err(got, want), cosine(got, want)
+    assert r <= MAX_REL and c >= MIN_COS, f"{what}: max-rel-err {r:.3e}, cosine {c:.7f}"
+    return r, c
