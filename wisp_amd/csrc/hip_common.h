@@ -31,7 +31,7 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));
  *     1032 * sum(x_even) + 1152 * sum(x_odd / 16)
  * over a block turns the sum into sum((n - 8) x) exactly in real
  * arithmetic. The excess itself is produced by one more MFMA against a
- * constant operand (see mfma_corr_operand).                                */
+ * constant operand (see mfma_excess_operand).                              */
 __device__ __forceinline__ h8 unpack8_magic(uint32_t w) {
     const uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, one024 = 0x64006400u;
     uint32_t t = w >> 8;
@@ -48,18 +48,20 @@ __device__ __host__ __forceinline__ int perm_slot(int e) {
     return ((e & 3) << 1) | (e >> 2);
 }
 
-/* Constant B operand for the correction MFMA: columns 0-7 carry the
- * excess pattern (1032 even / 1152 odd slots), columns 8-15 carry the
- * plain-sum pattern (1 / 16) used for the zero-point term. */
-__device__ __forceinline__ h8 mfma_corr_operand(int col) {
+/* Constant B operands for the correction MFMAs, the same in every column so
+ * that each lane receives its own token's value (no cross-lane read):
+ *   excess pattern: 1032 on even-element slots, 1152 on odd-element slots
+ *   sum pattern   : 1 / 16, giving sum(x) for the zero-point term.      */
+__device__ __forceinline__ h8 mfma_excess_operand() {
     h8 c;
-    if (col < 8) {
-        c[0] = (f16)1032.0f; c[1] = (f16)1032.0f; c[2] = (f16)1152.0f; c[3] = (f16)1152.0f;
-        c[4] = (f16)1032.0f; c[5] = (f16)1032.0f; c[6] = (f16)1152.0f; c[7] = (f16)1152.0f;
-    } else {
-        c[0] = (f16)1.0f; c[1] = (f16)1.0f; c[2] = (f16)16.0f; c[3] = (f16)16.0f;
-        c[4] = (f16)1.0f; c[5] = (f16)1.0f; c[6] = (f16)16.0f; c[7] = (f16)16.0f;
-    }
+    c[0] = (f16)1032.0f; c[1] = (f16)1032.0f; c[2] = (f16)1152.0f; c[3] = (f16)1152.0f;
+    c[4] = (f16)1032.0f; c[5] = (f16)1032.0f; c[6] = (f16)1152.0f; c[7] = (f16)1152.0f;
+    return c;
+}
+__device__ __forceinline__ h8 mfma_sum_operand() {
+    h8 c;
+    c[0] = (f16)1.0f; c[1] = (f16)1.0f; c[2] = (f16)16.0f; c[3] = (f16)16.0f;
+    c[4] = (f16)1.0f; c[5] = (f16)1.0f; c[6] = (f16)16.0f; c[7] = (f16)16.0f;
     return c;
 }
 

@@ -17,8 +17,9 @@
  *             ops per 8 values and feeds v_mfma_f32_16x16x32_f16 with the
  *             activations as the A operand (M of its 16 rows used) and the
  *             weights as B. One extra MFMA per block against a constant
- *             operand yields the magic-number excess and sum(x); the group
- *             scale and zero are applied per block in fp32. The K split is
+ *             operand yields the magic-number excess (a second one sum(x)
+ *             when zero points are present); the group scale and zero are
+ *             applied per block in fp32. The K split is
  *             reduced through LDS in a fixed order; the epilogue writes
  *             h' = w_route * silu(g) * u in fp16, already permuted for the
  *             down kernel.
@@ -149,12 +150,15 @@ __global__ __launch_bounds__(256) void decode_prep_kernel(DecodeParams P,
 
 /* One 128-element block for NT row tiles: xa[4] are this lane's activation
  * operands (token `col`, k-slice j), wv[s] the 16 B of nibbles of tile s.
- * Adds scale*(sum - excess) + zero*sum(x) into tot[s][v]. */
+ * Adds scale*(sum - excess) + zero*sum(x) into tot[s][v]. The excess and
+ * sum(x) come from MFMAs against constant operands that are equal in every
+ * column, so lane `col` holds them for its own tokens. */
 template <int M, int NG, int NT>
-__device__ __forceinline__ void block_step(const h8 (&xa)[4], const u4 (&wv)[NT], const h8 bc,
-                                           int gamma, const float (&sc)[NT][NG],
-                                           const float (&zc)[NT][NG], bool has_zeros,
-                                           float (&tot)[NT][M]) {
+__device__ __forceinline__ void block_step(const h8 (&xa)[4], const u4 (&wv)[NT], int gamma,
+                                           const float (&sc)[NT][NG], const float (&zc)[NT][NG],
+                                           bool has_zeros, float (&tot)[NT][M]) {
+    const h8 bex = mfma_excess_operand();
+    const h8 bsum = mfma_sum_operand();
 #pragma unroll
     for (int g = 0; g < NG; g++) {
         h8 xg[4];
@@ -163,9 +167,14 @@ __device__ __forceinline__ void block_step(const h8 (&xa)[4], const u4 (&wv)[NT]
             if (NG == 1 || gamma == g) xg[t] = xa[t];
             else xg[t] = (h8){0, 0, 0, 0, 0, 0, 0, 0};
         }
-        f4 corr = {0.f, 0.f, 0.f, 0.f};
+        f4 ex = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int t = 0; t < 4; t++) corr = mfma16x16x32(xg[t], bc, corr);
+        for (int t = 0; t < 4; t++) ex = mfma16x16x32(xg[t], bex, ex);
+        f4 xs = {0.f, 0.f, 0.f, 0.f};
+        if (has_zeros) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) xs = mfma16x16x32(xg[t], bsum, xs);
+        }
         f4 acc[NT];
 #pragma unroll
         for (int s = 0; s < NT; s++) {
@@ -175,14 +184,10 @@ __device__ __forceinline__ void block_step(const h8 (&xa)[4], const u4 (&wv)[NT]
         }
 #pragma unroll
         for (int v = 0; v < M; v++) {
-            float cv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                     __builtin_bit_cast(int, corr[v]), 0));
-            float xs = has_zeros ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                                 __builtin_bit_cast(int, corr[v]), 8))
-                                 : 0.0f;
 #pragma unroll
             for (int s = 0; s < NT; s++)
-                tot[s][v] = __builtin_fmaf(sc[s][g], acc[s][v] - cv, __builtin_fmaf(zc[s][g], xs, tot[s][v]));
+                tot[s][v] = __builtin_fmaf(sc[s][g], acc[s][v] - ex[v],
+                                           __builtin_fmaf(zc[s][g], xs[v], tot[s][v]));
         }
     }
 }
@@ -231,7 +236,6 @@ __global__ __launch_bounds__(64 * DEC_GU_MAX_WAVES) void gateup_kernel(const Dec
     }
     const bool xvalid = col < M;
     const uint16_t* xp = P.xperm + (size_t)(xvalid ? col : 0) * K + 32 * j;
-    const h8 bc = mfma_corr_operand(col);
 
     float tot[NT][M];
 #pragma unroll
@@ -264,7 +268,7 @@ __global__ __launch_bounds__(64 * DEC_GU_MAX_WAVES) void gateup_kernel(const Dec
                     zc[s][g] = P.has_zeros ? half_bits_to_float(zp[s][gi]) : 0.0f;
                 }
             }
-            block_step<M, NG, NT>(xa, wv, bc, gamma, sc, zc, P.has_zeros != 0, tot);
+            block_step<M, NG, NT>(xa, wv, gamma, sc, zc, P.has_zeros != 0, tot);
             if (more) {
 #pragma unroll
                 for (int s = 0; s < NT; s++) wv[s] = wn[s];
@@ -317,7 +321,6 @@ __global__ __launch_bounds__(1024) void down_kernel(const DecodeParams P, float*
     const int gpr = K / P.gs;
     const int gamma = (NG == 1) ? 0 : (j * NG) / 4;
     const bool xvalid = col < M;
-    const h8 bc = mfma_corr_operand(col);
 
     float tot[NT][M];
 #pragma unroll
@@ -360,7 +363,7 @@ __global__ __launch_bounds__(1024) void down_kernel(const DecodeParams P, float*
                     zc[s][g] = P.has_zeros ? half_bits_to_float(zp[s][gi]) : 0.0f;
                 }
             }
-            block_step<M, NG, NT>(xa, wv, bc, gamma, sc, zc, P.has_zeros != 0, tot);
+            block_step<M, NG, NT>(xa, wv, gamma, sc, zc, P.has_zeros != 0, tot);
         }
     }
     if (lane < 16) {
