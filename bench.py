@@ -28,7 +28,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E peak
-EV_ROUTE, EV_PREP, EV_GATEUP, EV_DOWN, EV_KINDS = 0, 1, 2, 3, 6
+EV_ROUTE, EV_PREP, EV_GATEUP, EV_DOWN, EV_COMBINE, EV_KINDS = 0, 1, 2, 3, 4, 7
 
 
 def log(msg):
@@ -152,7 +152,8 @@ def time_layer(layer, steps, warmup):
     lib.wisp_amd_set_kernel_events(None, 0)
     synchronize()
     kern = {}
-    for name, k in (("route", EV_ROUTE), ("prep", EV_PREP), ("gate_up", EV_GATEUP), ("down", EV_DOWN)):
+    for name, k in (("route", EV_ROUTE), ("prep", EV_PREP), ("gate_up", EV_GATEUP), ("down", EV_DOWN),
+                    ("combine", EV_COMBINE)):
         kern[name] = 1e3 * float(np.mean([evs[i][2 * k].elapsed_ms(evs[i][2 * k + 1]) for i in range(steps)]))
     return {"us_per_layer": 1e3 * dev_ms / steps, "host_us_per_layer": 1e3 * host_ms / steps,
             "kernel_us": kern}

@@ -123,7 +123,7 @@ int wisp_expert_layout_from_blob(const void* host_blob, size_t blob_size,
  * device address alignment: all sections 16-byte aligned for blob bases at
  * 8 mod 16 (the tier's slot placement), gate/up [inter, hidden], down
  * [hidden, inter], hidden and inter multiples of 128, group_size in
- * {32, 64} or a multiple of 128 dividing both. Else hipErrorInvalidValue. */
+ * a power of two >= 32 dividing both. Else hipErrorInvalidValue. */
 hipError_t wisp_expert_layout_check(const WispExpertLayout* L);
 
 /* ======================================================================= *
@@ -192,9 +192,10 @@ hipError_t wisp_gpu_moe_scatter(const float* d_y, const int* d_inv,
  *    out[t] = shared(x_t) + sum_k w[t,k] * expert_{idx[t,k]}(x_t)
  *    expert(x) = down . (silu(gate . x) * (up . x))
  *
- *    Two kernels after a small prep kernel: (a) gate+up+SiLU over every
- *    unique expert touched by the M tokens in one launch, (b) down
- *    projection and weighted combine for all of them in one launch.
+ *    A small prep kernel, then (a) gate+up+SiLU over every unique expert
+ *    touched by the M tokens in one launch, (b) the down projections of all
+ *    of them in one launch, (c) a fixed-order combine of the per-expert
+ *    outputs (routing weights are folded in before the down projection).
  *    Weights stream from the blobs in place; nothing is dequantised to
  *    memory. Routing stays on the device.
  * ======================================================================= */
@@ -233,7 +234,7 @@ hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table,
 /* When events != NULL, the fused launchers record events[2*k] before and
  * events[2*k+1] after each kernel of kind k < n_pairs on the launch stream:
  * k = 0 router (wisp_gpu_moe_route), 1 decode prep, 2 decode gate/up,
- * 3 decode down, 4 prefill gate/up, 5 prefill down. Process-wide; for
+ * 3 decode down, 4 decode combine, 5 prefill gate/up, 6 prefill down. Process-wide; for
  * timing runs only; not thread-safe. */
 void wisp_amd_set_kernel_events(hipEvent_t* events, int n_pairs);
 

@@ -32,14 +32,18 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));
  * over a block turns the sum into sum((n - 8) x) exactly in real
  * arithmetic. The excess itself is produced by one more MFMA against a
  * constant operand (see mfma_excess_operand).                              */
-__device__ __forceinline__ h8 unpack8_magic(uint32_t w) {
-    const uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, one024 = 0x64006400u;
-    uint32_t t = w >> 8;
+/* Written in bitfield-insert form, (w & m) | (o & ~m), which equals
+ * (w & m) | o for these masks, with m and o taken from kernel arguments:
+ * the compiler then emits one v_bfi_b32 per output dword (with literal
+ * masks it emits v_and_b32 + v_or_b32). */
+__device__ __forceinline__ h8 unpack8_magic(uint32_t w, uint32_t m_lo, uint32_t m_hi,
+                                            uint32_t one024) {
+    const uint32_t t = w >> 8;
     u4 v;
-    v.x = (w & m_lo) | one024;
-    v.y = (w & m_hi) | one024;
-    v.z = (t & m_lo) | one024;
-    v.w = (t & m_hi) | one024;
+    v.x = (w & m_lo) | (one024 & ~m_lo);
+    v.y = (w & m_hi) | (one024 & ~m_hi);
+    v.z = (t & m_lo) | (one024 & ~m_lo);
+    v.w = (t & m_hi) | (one024 & ~m_hi);
     return __builtin_bit_cast(h8, v);
 }
 
@@ -88,8 +92,8 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
 
 /* ---- profiling hook (wisp_amd_set_kernel_events) -----------------------
  * Fixed event-pair slot per kernel kind. */
-enum { EV_ROUTE = 0, EV_PREP = 1, EV_GATEUP = 2, EV_DOWN = 3, EV_PF_GATEUP = 4, EV_PF_DOWN = 5,
-       EV_KINDS = 6 };
+enum { EV_ROUTE = 0, EV_PREP = 1, EV_GATEUP = 2, EV_DOWN = 3, EV_COMBINE = 4, EV_PF_GATEUP = 5,
+       EV_PF_DOWN = 6, EV_KINDS = 7 };
 extern "C" hipEvent_t* wisp_amd__events;
 extern "C" int wisp_amd__event_pairs;
 

@@ -35,19 +35,22 @@
 
 #define DEC_MAX_TOKENS 4
 #define DEC_MAX_TOPK 64
-#define DEC_MAX_WAVES 16
-#define DEC_GU_TILES 1
-#define DEC_GU_MAX_WAVES 8
+#define DEC_MAX_WAVES 8
+#define DEC_CHUNK_BLOCKS 32   /* down-projection K chunk per workgroup: 4096 elements */
 
 struct DecodeParams {
     uint64_t p_off[3], s_off[3], z_off[3];
     int hidden, inter, gs, has_zeros;
+    int gshift;           /* log2(gs * NG / 128): block -> group index */
+    int n_chunks;         /* down-projection K chunks: ceil(inter/128 / DEC_CHUNK_BLOCKS) */
+    uint32_t m_lo, m_hi, one024;  /* unpack masks 0x000F000F, 0x00F000F0, 0x64006400 */
     int max_u;
     int* n_unique;
     const uint8_t** ublob;
     float* uw;            /* [max_u][4] routing weight of each token     */
     uint16_t* xperm;      /* [M][hidden] permuted fp16 activations        */
     uint16_t* hperm;      /* [max_u][M][inter] permuted fp16 h'           */
+    float* part;          /* [max_u][n_chunks][M][hidden] down partials   */
 };
 
 /* ======================================================================= */
@@ -145,18 +148,20 @@ __global__ __launch_bounds__(256) void decode_prep_kernel(DecodeParams P,
 }
 
 /* ======================================================================= */
-/* shared MFMA block step                                                   */
+/* shared streaming machinery                                               */
 /* ======================================================================= */
 
 /* One 128-element block for NT row tiles: xa[4] are this lane's activation
  * operands (token `col`, k-slice j), wv[s] the 16 B of nibbles of tile s.
  * Adds scale*(sum - excess) + zero*sum(x) into tot[s][v]. The excess and
  * sum(x) come from MFMAs against constant operands that are equal in every
- * column, so lane `col` holds them for its own tokens. */
-template <int M, int NG, int NT>
+ * column, so lane `col` holds them for its own tokens. A block with
+ * live == false (a padding slot of the unrolled loop) adds nothing. */
+template <int M, int NG, int NT, bool HZ>
 __device__ __forceinline__ void block_step(const h8 (&xa)[4], const u4 (&wv)[NT], int gamma,
                                            const float (&sc)[NT][NG], const float (&zc)[NT][NG],
-                                           bool has_zeros, float (&tot)[NT][M]) {
+                                           bool live, uint32_t m_lo, uint32_t m_hi,
+                                           uint32_t one024, float (&tot)[NT][M]) {
     const h8 bex = mfma_excess_operand();
     const h8 bsum = mfma_sum_operand();
 #pragma unroll
@@ -171,7 +176,7 @@ __device__ __forceinline__ void block_step(const h8 (&xa)[4], const u4 (&wv)[NT]
 #pragma unroll
         for (int t = 0; t < 4; t++) ex = mfma16x16x32(xg[t], bex, ex);
         f4 xs = {0.f, 0.f, 0.f, 0.f};
-        if (has_zeros) {
+        if (HZ) {
 #pragma unroll
             for (int t = 0; t < 4; t++) xs = mfma16x16x32(xg[t], bsum, xs);
         }
@@ -180,24 +185,132 @@ __device__ __forceinline__ void block_step(const h8 (&xa)[4], const u4 (&wv)[NT]
         for (int s = 0; s < NT; s++) {
             acc[s] = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int t = 0; t < 4; t++) acc[s] = mfma16x16x32(xg[t], unpack8_magic(wv[s][t]), acc[s]);
+            for (int t = 0; t < 4; t++)
+                acc[s] = mfma16x16x32(xg[t], unpack8_magic(wv[s][t], m_lo, m_hi, one024), acc[s]);
         }
 #pragma unroll
-        for (int v = 0; v < M; v++) {
+        for (int s = 0; s < NT; s++) {
+            const float scl = live ? sc[s][g] : 0.0f;
+            const float zcl = live ? zc[s][g] : 0.0f;
 #pragma unroll
-            for (int s = 0; s < NT; s++)
-                tot[s][v] = __builtin_fmaf(sc[s][g], acc[s][v] - ex[v],
-                                           __builtin_fmaf(zc[s][g], xs[v], tot[s][v]));
+            for (int v = 0; v < M; v++) {
+                float t = __builtin_fmaf(scl, acc[s][v] - ex[v], tot[s][v]);
+                if (HZ) t = __builtin_fmaf(zcl, xs[v], t);
+                tot[s][v] = t;
+            }
         }
     }
 }
 
+/* LDS image of one workgroup's operands:
+ *   x    [M][XR] fp16  permuted activations of the staged K range, rows
+ *                      padded by 32 halves so tokens fall in different banks
+ *   sc   [NT][16][GS]  raw fp16 scale bits of the tile rows for the staged
+ *   zc   [NT][16][GS]  groups (zeros only when present)
+ *   red  [waves][NT][16][M] fp32 K-split partials                        */
+struct LdsMap {
+    int XR, GS;
+    int x_off, sc_off, zc_off, red_off, bytes;
+};
+
+__host__ __device__ inline LdsMap lds_map(int M, int NT, int xk, int gs_count, bool hz, int waves) {
+    LdsMap L;
+    L.XR = xk + 32;
+    L.GS = gs_count;
+    int off = 0;
+    L.x_off = off;
+    off += M * L.XR * 2;
+    off = (off + 15) & ~15;
+    L.sc_off = off;
+    off += NT * 16 * gs_count * 2;
+    off = (off + 15) & ~15;
+    L.zc_off = off;
+    if (hz) off += NT * 16 * gs_count * 2;
+    off = (off + 15) & ~15;
+    L.red_off = off;
+    off += waves * NT * 16 * M * 4;
+    L.bytes = (off + 15) & ~15;
+    return L;
+}
+
+/* Copies M activation rows (K range [k0, k0 + xk) of rows of length K) into
+ * the LDS x image with 16-byte accesses. */
 template <int M>
-__device__ __forceinline__ void load_x4(h8 (&xa)[4], const uint16_t* p, bool valid) {
+__device__ __forceinline__ void stage_x(uint8_t* smem, const LdsMap& L, const uint16_t* src, int K,
+                                        int k0, int xk) {
+    uint16_t* xs = (uint16_t*)(smem + L.x_off);
+    const int per_row = xk / 8;
+    for (int i = threadIdx.x; i < M * per_row; i += blockDim.x) {
+        const int v = i / per_row, c = i - v * per_row;
+        *(u4*)(xs + v * L.XR + c * 8) = *(const u4*)(src + (size_t)v * K + k0 + c * 8);
+    }
+}
+
+/* Copies the raw scale (or zero) bits of 16 consecutive rows starting at
+ * row r0 of a [rows][G] fp16 table, groups [g0, g0 + gn), into dst[16][gn]. */
+__device__ __forceinline__ void stage_groups(uint16_t* dst, const uint16_t* tab, int G, int r0,
+                                             int g0, int gn) {
+    for (int i = threadIdx.x; i < 16 * gn; i += blockDim.x) {
+        const int r = i / gn, g = i - r * gn;
+        dst[i] = tab[(size_t)(r0 + r) * G + g0 + g];
+    }
+}
+
+/* Streams blocks [b0, b1) (absolute block indices of the weight rows) of NT
+ * row tiles into tot, in batches of PF blocks: the weight loads of a whole
+ * batch are issued first, then the batch is computed. No load result is
+ * carried across loop iterations, so the compiler never has to copy (and
+ * therefore wait on) an in-flight register; latency is covered by the other
+ * resident waves. Activations and scales come from the LDS image, whose K
+ * range starts at block xb0 and whose groups start at g_lo. The last batch
+ * clamps its loads to the last block (the repeats hit in cache) and
+ * computes its padding slots with zero scale. */
+template <int M, int NG, int NT, int PF, bool HZ>
+__device__ __forceinline__ void stream_blocks(const uint8_t* const (&wp)[NT], const uint8_t* smem,
+                                              const LdsMap& L, int b0, int b1, int xb0, int g_lo,
+                                              int gshift, int col, int j, uint32_t m_lo,
+                                              uint32_t m_hi, uint32_t one024,
+                                              float (&tot)[NT][M]) {
+    constexpr int B = PF;
+    if (b0 >= b1) return;
+    /* A VALU op reads at most one scalar operand on this target: with the
+     * masks in SGPRs every bitfield insert of the unpack splits into an and
+     * plus an or. Pinning them to VGPRs (an empty asm emits no instruction)
+     * lets each output dword be one v_and_or_b32. */
+    asm volatile("" : "+v"(m_lo));
+    asm volatile("" : "+v"(m_hi));
+    asm volatile("" : "+v"(one024));
+    const uint16_t* xs = (const uint16_t*)(smem + L.x_off) + (col < M ? col : 0) * L.XR + 32 * j;
+    const uint16_t* scs = (const uint16_t*)(smem + L.sc_off) + col * L.GS;
+    const uint16_t* zcs = (const uint16_t*)(smem + L.zc_off) + col * L.GS;
+    const int gamma = (j * NG) / 4;
+    for (int base = b0; base < b1; base += B) {
+        u4 w[B][NT];
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-        if (valid) xa[t] = *(const h8*)(p + 8 * t);
-        else xa[t] = (h8){0, 0, 0, 0, 0, 0, 0, 0};
+        for (int p = 0; p < B; p++) {
+            const int bb = min(base + p, b1 - 1);
+#pragma unroll
+            for (int s = 0; s < NT; s++) w[p][s] = *(const u4*)(wp[s] + (size_t)bb * 64);
+        }
+#pragma unroll
+        for (int p = 0; p < B; p++) {
+            const int b = base + p;
+            const int bc = min(b, b1 - 1);
+            h8 xa[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) xa[t] = *(const h8*)(xs + (bc - xb0) * 128 + 8 * t);
+            float sc[NT][NG], zc[NT][NG];
+#pragma unroll
+            for (int g = 0; g < NG; g++) {
+                const int gi = ((bc * NG + g) >> gshift) - g_lo;
+#pragma unroll
+                for (int s = 0; s < NT; s++) {
+                    sc[s][g] = half_bits_to_float(scs[s * 16 * L.GS + gi]);
+                    zc[s][g] = HZ ? half_bits_to_float(zcs[s * 16 * L.GS + gi]) : 0.0f;
+                }
+            }
+            block_step<M, NG, NT, HZ>(xa, w[p], gamma, sc, zc, b < b1, m_lo, m_hi, one024, tot);
+        }
     }
 }
 
@@ -205,11 +318,12 @@ __device__ __forceinline__ void load_x4(h8 (&xa)[4], const uint16_t* p, bool val
 /* gate/up + SiLU                                                           */
 /* ======================================================================= */
 
-template <int M, int NG>
-__global__ __launch_bounds__(64 * DEC_GU_MAX_WAVES) void gateup_kernel(const DecodeParams P) {
-    constexpr int TILES = DEC_GU_TILES;
+/* grid (inter / (16 TILES), max_u); workgroup = TILES gate + TILES up row
+ * tiles of unique expert blockIdx.y over the full hidden K, waves split K. */
+template <int M, int NG, int TILES, int PF, bool HZ>
+__global__ __launch_bounds__(64 * DEC_MAX_WAVES) void gateup_kernel(const DecodeParams P) {
     constexpr int NT = 2 * TILES;
-    __shared__ float red[DEC_GU_MAX_WAVES][NT][16][M];
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int u = blockIdx.y;
     if (u >= *P.n_unique) return;
     const uint8_t* blob = P.ublob[u];
@@ -218,78 +332,51 @@ __global__ __launch_bounds__(64 * DEC_GU_MAX_WAVES) void gateup_kernel(const Dec
     const int col = lane & 15, j = lane >> 4;
     const int r0 = blockIdx.x * 16 * TILES;
     const int nblk = K >> 7;
+    const int G = K / P.gs;
     const int b0 = wave * nblk / nw, b1 = (wave + 1) * nblk / nw;
-    const size_t row_bytes = (size_t)K / 2;
-    const int gpr = K / P.gs;
-    const int gamma = (NG == 1) ? 0 : (j * NG) / 4;
+    const LdsMap L = lds_map(M, NT, K, G, HZ, nw);
 
     const uint8_t* wp[NT];
-    const uint16_t* sp[NT];
-    const uint16_t* zp[NT];
 #pragma unroll
     for (int s = 0; s < NT; s++) {
         const int mat = s < TILES ? 0 : 1;
-        const int row = r0 + 16 * (s % TILES) + col;
-        wp[s] = blob + P.p_off[mat] + (size_t)row * row_bytes + 16 * j;
-        sp[s] = (const uint16_t*)(blob + P.s_off[mat]) + (size_t)row * gpr;
-        zp[s] = (const uint16_t*)(blob + P.z_off[mat]) + (size_t)row * gpr;
+        wp[s] = blob + P.p_off[mat] + (size_t)(r0 + 16 * (s % TILES) + col) * (K / 2) + 16 * j;
     }
-    const bool xvalid = col < M;
-    const uint16_t* xp = P.xperm + (size_t)(xvalid ? col : 0) * K + 32 * j;
+    stage_x<M>(smem, L, P.xperm, K, 0, K);
+#pragma unroll
+    for (int s = 0; s < NT; s++) {
+        const int mat = s < TILES ? 0 : 1;
+        const int rt = r0 + 16 * (s % TILES);
+        stage_groups((uint16_t*)(smem + L.sc_off) + s * 16 * G,
+                     (const uint16_t*)(blob + P.s_off[mat]), G, rt, 0, G);
+        if (HZ)
+            stage_groups((uint16_t*)(smem + L.zc_off) + s * 16 * G,
+                         (const uint16_t*)(blob + P.z_off[mat]), G, rt, 0, G);
+    }
+    __syncthreads();
 
     float tot[NT][M];
 #pragma unroll
     for (int s = 0; s < NT; s++)
 #pragma unroll
         for (int v = 0; v < M; v++) tot[s][v] = 0.0f;
+    stream_blocks<M, NG, NT, PF, HZ>(wp, smem, L, b0, b1, 0, 0, P.gshift, col, j, P.m_lo, P.m_hi,
+                                     P.one024, tot);
 
-    if (b0 < b1) {
-        u4 wv[NT];
-        h8 xa[4];
-#pragma unroll
-        for (int s = 0; s < NT; s++) wv[s] = *(const u4*)(wp[s] + (size_t)b0 * 64);
-        load_x4<M>(xa, xp + (size_t)b0 * 128, xvalid);
-        for (int b = b0; b < b1; b++) {
-            u4 wn[NT];
-            h8 xn[4];
-            const bool more = b + 1 < b1;
-            if (more) {
-#pragma unroll
-                for (int s = 0; s < NT; s++) wn[s] = *(const u4*)(wp[s] + (size_t)(b + 1) * 64);
-                load_x4<M>(xn, xp + (size_t)(b + 1) * 128, xvalid);
-            }
-            float sc[NT][NG], zc[NT][NG];
-#pragma unroll
-            for (int g = 0; g < NG; g++) {
-                const int gi = (b * 128 + g * (128 / NG)) / P.gs;
-#pragma unroll
-                for (int s = 0; s < NT; s++) {
-                    sc[s][g] = half_bits_to_float(sp[s][gi]);
-                    zc[s][g] = P.has_zeros ? half_bits_to_float(zp[s][gi]) : 0.0f;
-                }
-            }
-            block_step<M, NG, NT>(xa, wv, gamma, sc, zc, P.has_zeros != 0, tot);
-            if (more) {
-#pragma unroll
-                for (int s = 0; s < NT; s++) wv[s] = wn[s];
-#pragma unroll
-                for (int t = 0; t < 4; t++) xa[t] = xn[t];
-            }
-        }
-    }
+    float* red = (float*)(smem + L.red_off);
     if (lane < 16) {
 #pragma unroll
         for (int s = 0; s < NT; s++)
 #pragma unroll
-            for (int v = 0; v < M; v++) red[wave][s][col][v] = tot[s][v];
+            for (int v = 0; v < M; v++) red[((wave * NT + s) * 16 + col) * M + v] = tot[s][v];
     }
     __syncthreads();
     for (int o = threadIdx.x; o < TILES * 16 * M; o += blockDim.x) {
         const int v = o % M, rc = o / M, q = rc / 16, c = rc % 16;
         float g = 0.0f, up = 0.0f;
         for (int ww = 0; ww < nw; ww++) {
-            g += red[ww][q][c][v];
-            up += red[ww][TILES + q][c][v];
+            g += red[((ww * NT + q) * 16 + c) * M + v];
+            up += red[((ww * NT + TILES + q) * 16 + c) * M + v];
         }
         const float h = silu_f(g) * up * P.uw[u * 4 + v];
         const int r = r0 + 16 * q + c;
@@ -301,90 +388,89 @@ __global__ __launch_bounds__(64 * DEC_GU_MAX_WAVES) void gateup_kernel(const Dec
 }
 
 /* ======================================================================= */
-/* down + combine                                                           */
+/* down (per expert and K chunk) + combine                                  */
 /* ======================================================================= */
 
-template <int M, int NG, int TILES>
-__global__ __launch_bounds__(1024) void down_kernel(const DecodeParams P, float* out32,
-                                                    uint16_t* out16, int accumulate) {
+/* grid (hidden / (16 TILES), max_u * n_chunks): workgroup (row tile,
+ * unique expert u, K chunk c of DEC_CHUNK_BLOCKS blocks) writes
+ * part[u][c][v][row] = down_u[row, chunk] . h'_u[v][chunk] (routing weight
+ * already folded into h'). */
+template <int M, int NG, int TILES, int PF, bool HZ>
+__global__ __launch_bounds__(64 * DEC_MAX_WAVES) void down_kernel(const DecodeParams P) {
     constexpr int NT = TILES;
-    __shared__ float red[DEC_MAX_WAVES][NT][16][M];
-    const int n_u = *P.n_unique;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int nch = P.n_chunks;
+    const int u = blockIdx.y / nch, c = blockIdx.y - u * nch;
+    if (u >= *P.n_unique) return;
+    const uint8_t* blob = P.ublob[u];
     const int K = P.inter, H = P.hidden;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int col = lane & 15, j = lane >> 4;
     const int r0 = blockIdx.x * 16 * TILES;
-    const int bpe = K >> 7;
-    const int NB = n_u * bpe;
-    const int b0 = wave * NB / nw, b1 = (wave + 1) * NB / nw;
-    const size_t row_bytes = (size_t)K / 2;
-    const int gpr = K / P.gs;
-    const int gamma = (NG == 1) ? 0 : (j * NG) / 4;
-    const bool xvalid = col < M;
+    const int nblk = K >> 7;
+    const int G = K / P.gs;
+    const int cb0 = c * DEC_CHUNK_BLOCKS, cb1 = min(cb0 + DEC_CHUNK_BLOCKS, nblk);
+    const int g_lo = (cb0 * NG) >> P.gshift, g_hi = (((cb1 * NG) - 1) >> P.gshift) + 1;
+    const int nb = cb1 - cb0;
+    const int b0 = cb0 + wave * nb / nw, b1 = cb0 + (wave + 1) * nb / nw;
+    const LdsMap L = lds_map(M, NT, DEC_CHUNK_BLOCKS * 128, g_hi - g_lo, HZ, nw);
+
+    const uint8_t* wp[NT];
+#pragma unroll
+    for (int s = 0; s < NT; s++)
+        wp[s] = blob + P.p_off[2] + (size_t)(r0 + 16 * s + col) * (K / 2) + 16 * j;
+    stage_x<M>(smem, L, P.hperm + (size_t)u * M * K, K, cb0 * 128, nb * 128);
+#pragma unroll
+    for (int s = 0; s < NT; s++) {
+        stage_groups((uint16_t*)(smem + L.sc_off) + s * 16 * L.GS,
+                     (const uint16_t*)(blob + P.s_off[2]), G, r0 + 16 * s, g_lo, L.GS);
+        if (HZ)
+            stage_groups((uint16_t*)(smem + L.zc_off) + s * 16 * L.GS,
+                         (const uint16_t*)(blob + P.z_off[2]), G, r0 + 16 * s, g_lo, L.GS);
+    }
+    __syncthreads();
 
     float tot[NT][M];
 #pragma unroll
     for (int s = 0; s < NT; s++)
 #pragma unroll
         for (int v = 0; v < M; v++) tot[s][v] = 0.0f;
+    stream_blocks<M, NG, NT, PF, HZ>(wp, smem, L, b0, b1, cb0, g_lo, P.gshift, col, j, P.m_lo,
+                                     P.m_hi, P.one024, tot);
 
-    if (b0 < b1) {
-        int cur_u = -1;
-        const uint8_t* wp[NT];
-        const uint16_t* sp[NT];
-        const uint16_t* zp[NT];
-        const uint16_t* xp = nullptr;
-        u4 wv[NT];
-        h8 xa[4];
-        for (int gb = b0; gb < b1; gb++) {
-            const int uu = gb / bpe, b = gb - uu * bpe;
-            if (uu != cur_u) {
-                cur_u = uu;
-                const uint8_t* blob = P.ublob[uu];
-#pragma unroll
-                for (int s = 0; s < NT; s++) {
-                    const int row = r0 + 16 * s + col;
-                    wp[s] = blob + P.p_off[2] + (size_t)row * row_bytes + 16 * j;
-                    sp[s] = (const uint16_t*)(blob + P.s_off[2]) + (size_t)row * gpr;
-                    zp[s] = (const uint16_t*)(blob + P.z_off[2]) + (size_t)row * gpr;
-                }
-                xp = P.hperm + ((size_t)uu * M + (xvalid ? col : 0)) * K + 32 * j;
-            }
-#pragma unroll
-            for (int s = 0; s < NT; s++) wv[s] = *(const u4*)(wp[s] + (size_t)b * 64);
-            load_x4<M>(xa, xp + (size_t)b * 128, xvalid);
-            float sc[NT][NG], zc[NT][NG];
-#pragma unroll
-            for (int g = 0; g < NG; g++) {
-                const int gi = (b * 128 + g * (128 / NG)) / P.gs;
-#pragma unroll
-                for (int s = 0; s < NT; s++) {
-                    sc[s][g] = half_bits_to_float(sp[s][gi]);
-                    zc[s][g] = P.has_zeros ? half_bits_to_float(zp[s][gi]) : 0.0f;
-                }
-            }
-            block_step<M, NG, NT>(xa, wv, gamma, sc, zc, P.has_zeros != 0, tot);
-        }
-    }
+    float* red = (float*)(smem + L.red_off);
     if (lane < 16) {
 #pragma unroll
         for (int s = 0; s < NT; s++)
 #pragma unroll
-            for (int v = 0; v < M; v++) red[wave][s][col][v] = tot[s][v];
+            for (int v = 0; v < M; v++) red[((wave * NT + s) * 16 + col) * M + v] = tot[s][v];
     }
     __syncthreads();
     for (int o = threadIdx.x; o < TILES * 16 * M; o += blockDim.x) {
-        const int v = o % M, rc = o / M, q = rc / 16, c = rc % 16;
+        const int v = o % M, rc = o / M, q = rc / 16, cc = rc % 16;
         float y = 0.0f;
-        for (int ww = 0; ww < nw; ww++) y += red[ww][q][c][v];
-        const int r = r0 + 16 * q + c;
-        const size_t oi = (size_t)v * H + r;
-        if (out32) {
-            if (accumulate) y += out32[oi];
-            out32[oi] = y;
-        }
-        if (out16) out16[oi] = __builtin_bit_cast(uint16_t, (f16)y);
+        for (int ww = 0; ww < nw; ww++) y += red[((ww * NT + q) * 16 + cc) * M + v];
+        P.part[(((size_t)u * nch + c) * M + v) * H + r0 + 16 * q + cc] = y;
     }
+}
+
+/* out[v][r] (+)= sum over unique experts u (list order) and K chunks c of
+ * part[u][c][v][r]. */
+__global__ __launch_bounds__(256) void combine_kernel(const DecodeParams P, int M, float* out32,
+                                                      uint16_t* out16, int accumulate) {
+    const int n_u = *P.n_unique;
+    const int H = P.hidden, nch = P.n_chunks;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= M * H) return;
+    const int v = i / H, r = i - v * H;
+    float y = 0.0f;
+    for (int u = 0; u < n_u; u++)
+        for (int c = 0; c < nch; c++) y += P.part[(((size_t)u * nch + c) * M + v) * H + r];
+    if (out32) {
+        if (accumulate) y += out32[i];
+        out32[i] = y;
+    }
+    if (out16) out16[i] = __builtin_bit_cast(uint16_t, (f16)y);
 }
 
 /* ======================================================================= */
@@ -399,7 +485,7 @@ extern "C" hipError_t wisp_expert_layout_check(const WispExpertLayout* L) {
         return hipErrorInvalidValue;
     if (inter == 0 || hidden == 0 || inter % 128 || hidden % 128) return hipErrorInvalidValue;
     const uint64_t gs = L->group_size;
-    const bool gs_ok = gs == 32 || gs == 64 || (gs >= 128 && gs % 128 == 0);
+    const bool gs_ok = gs >= 32 && (gs & (gs - 1)) == 0;
     if (!gs_ok || hidden % gs || inter % gs) return hipErrorInvalidValue;
     for (int m = 0; m < 3; m++) {
         const uint64_t n = (uint64_t)L->rows[m] * L->cols[m];
@@ -413,7 +499,7 @@ extern "C" hipError_t wisp_expert_layout_check(const WispExpertLayout* L) {
 }
 
 struct WsLayout {
-    size_t nu, ublob, uw, xperm, hperm, total;
+    size_t nu, ublob, uw, xperm, hperm, part, total;
     int max_u;
 };
 
@@ -426,6 +512,8 @@ static WsLayout ws_layout(const WispExpertLayout* L, int M, int top_k, int has_s
     w.uw = off; off = align_up(off + (size_t)w.max_u * 4 * sizeof(float), 256);
     w.xperm = off; off = align_up(off + (size_t)M * L->cols[0] * 2, 256);
     w.hperm = off; off = align_up(off + (size_t)w.max_u * M * L->rows[0] * 2, 256);
+    const size_t nch = ((L->rows[0] / 128) + DEC_CHUNK_BLOCKS - 1) / DEC_CHUNK_BLOCKS;
+    w.part = off; off = align_up(off + (size_t)w.max_u * nch * M * L->cols[0] * 4, 256);
     w.total = off;
     return w;
 }
@@ -437,33 +525,103 @@ extern "C" size_t wisp_moe_decode_workspace_bytes(const WispExpertLayout* L, int
     return ws_layout(L, n_tokens, top_k, has_shared).total;
 }
 
-template <int M, int NG>
-static void launch_compute(const DecodeParams& P, int gu_waves, int dn_waves, float* out32,
-                           uint16_t* out16, int accumulate, hipStream_t s) {
-    ev_before(EV_GATEUP, s);
-    hipLaunchKernelGGL((gateup_kernel<M, NG>), dim3(P.inter / (16 * DEC_GU_TILES), P.max_u),
-                       dim3(64 * gu_waves), 0, s, P);
-    ev_after(EV_GATEUP, s);
-    ev_before(EV_DOWN, s);
-    hipLaunchKernelGGL((down_kernel<M, NG, 1>), dim3(P.hidden / 16), dim3(64 * dn_waves), 0, s,
-                       P, out32, out16, accumulate);
-    ev_after(EV_DOWN, s);
+/* Launch shape of the two expert kernels. Values <= 0 select the built-in
+ * heuristic. Set only through wisp_amd__decode_config (tuning sweeps). */
+struct DecodeCfg {
+    int gu_tiles, gu_waves, gu_pf, dn_tiles, dn_waves, dn_pf;
+};
+static DecodeCfg g_dec_cfg = {0, 0, 0, 0, 0, 0};
+
+extern "C" void wisp_amd__decode_config(int gu_tiles, int gu_waves, int gu_pf, int dn_tiles,
+                                        int dn_waves, int dn_pf) {
+    g_dec_cfg = {gu_tiles, gu_waves, gu_pf, dn_tiles, dn_waves, dn_pf};
 }
 
-template <int M>
-static void launch_ng(int ng, const DecodeParams& P, int gw, int dw, float* o32, uint16_t* o16,
-                      int acc, hipStream_t s) {
-    if (ng == 1) launch_compute<M, 1>(P, gw, dw, o32, o16, acc, s);
-    else if (ng == 2) launch_compute<M, 2>(P, gw, dw, o32, o16, acc, s);
-    else launch_compute<M, 4>(P, gw, dw, o32, o16, acc, s);
-}
-
-/* Waves per workgroup for a K split: about 4 blocks of 128 per wave. */
-static int clamp_waves(int blocks_total, int max_waves) {
-    int w = blocks_total / 4;
+/* Waves per workgroup so that each wave streams about `per_wave` blocks. */
+static int waves_for(int blocks_total, int per_wave, int max_waves) {
+    int w = blocks_total / per_wave;
     if (w < 1) w = 1;
     if (w > max_waves) w = max_waves;
     return w;
+}
+
+template <int M, int NG, int TILES, int PF, bool HZ>
+static void launch_gateup(const DecodeParams& P, int waves, hipStream_t s) {
+    const LdsMap L = lds_map(M, 2 * TILES, P.hidden, P.hidden / P.gs, HZ, waves);
+    auto k = gateup_kernel<M, NG, TILES, PF, HZ>;
+    if (L.bytes > 65536)
+        (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, L.bytes);
+    hipLaunchKernelGGL(k, dim3(P.inter / (16 * TILES), P.max_u), dim3(64 * waves), L.bytes, s, P);
+}
+
+template <int M, int NG, int TILES, int PF, bool HZ>
+static void launch_down(const DecodeParams& P, int waves, hipStream_t s) {
+    /* LDS sized for the largest chunk: full DEC_CHUNK_BLOCKS and its groups */
+    const int ng_hi = (((DEC_CHUNK_BLOCKS * NG) - 1) >> P.gshift) + 2;
+    const LdsMap L = lds_map(M, TILES, DEC_CHUNK_BLOCKS * 128, ng_hi, HZ, waves);
+    auto k = down_kernel<M, NG, TILES, PF, HZ>;
+    if (L.bytes > 65536)
+        (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, L.bytes);
+    hipLaunchKernelGGL(k, dim3(P.hidden / (16 * TILES), P.max_u * P.n_chunks), dim3(64 * waves),
+                       L.bytes, s, P);
+}
+
+template <int M, int NG, bool HZ>
+static void launch_compute(const DecodeParams& P, float* out32, uint16_t* out16, int accumulate,
+                           hipStream_t s) {
+    const DecodeCfg c = g_dec_cfg;
+    const int gu_waves = c.gu_waves > 0 ? (c.gu_waves > DEC_MAX_WAVES ? DEC_MAX_WAVES : c.gu_waves)
+                                        : waves_for(P.hidden / 128, 8, 4);
+    const int chunk = (P.inter / 128) < DEC_CHUNK_BLOCKS ? (P.inter / 128) : DEC_CHUNK_BLOCKS;
+    const int dn_waves = c.dn_waves > 0 ? (c.dn_waves > DEC_MAX_WAVES ? DEC_MAX_WAVES : c.dn_waves)
+                                        : waves_for(chunk, 8, 4);
+    /* Defaults (measured on MI355X at the Mixtral and DeepSeek-V3 decode
+     * shapes): one row tile per matrix, batches of 2 blocks, about 8 blocks
+     * per wave and at most 4 waves. Other tile / batch variants are built
+     * for the common case only (group size >= 128, no zero points). */
+    auto variant = [](int tiles, int pf) { return 10 * (tiles == 2 ? 2 : 1) + (pf == 8 ? 8 : (pf == 4 ? 4 : 2)); };
+    const int gv = (NG == 1 && !HZ) ? variant(c.gu_tiles, c.gu_pf) : 0;
+    const int dv = (NG == 1 && !HZ) ? variant(c.dn_tiles, c.dn_pf) : 0;
+    ev_before(EV_GATEUP, s);
+    switch (gv) {
+        case 12: launch_gateup<M, 1, 1, 2, false>(P, gu_waves, s); break;
+        case 14: launch_gateup<M, 1, 1, 4, false>(P, gu_waves, s); break;
+        case 18: launch_gateup<M, 1, 1, 8, false>(P, gu_waves, s); break;
+        case 22: launch_gateup<M, 1, 2, 2, false>(P, gu_waves, s); break;
+        case 24: launch_gateup<M, 1, 2, 4, false>(P, gu_waves, s); break;
+        default: launch_gateup<M, NG, 1, 2, HZ>(P, gu_waves, s); break;
+    }
+    ev_after(EV_GATEUP, s);
+    ev_before(EV_DOWN, s);
+    switch (dv) {
+        case 12: launch_down<M, 1, 1, 2, false>(P, dn_waves, s); break;
+        case 14: launch_down<M, 1, 1, 4, false>(P, dn_waves, s); break;
+        case 18: launch_down<M, 1, 1, 8, false>(P, dn_waves, s); break;
+        case 22: launch_down<M, 1, 2, 2, false>(P, dn_waves, s); break;
+        case 24: launch_down<M, 1, 2, 4, false>(P, dn_waves, s); break;
+        default: launch_down<M, NG, 1, 2, HZ>(P, dn_waves, s); break;
+    }
+    ev_after(EV_DOWN, s);
+    ev_before(EV_COMBINE, s);
+    const int n = M * P.hidden;
+    hipLaunchKernelGGL(combine_kernel, dim3((n + 255) / 256), dim3(256), 0, s, P, M, out32, out16,
+                       accumulate);
+    ev_after(EV_COMBINE, s);
+}
+
+template <int M>
+static void launch_ng(int ng, bool hz, const DecodeParams& P, float* o32, uint16_t* o16, int acc,
+                      hipStream_t s) {
+    if (ng == 1) {
+        if (hz) launch_compute<M, 1, true>(P, o32, o16, acc, s);
+        else launch_compute<M, 1, false>(P, o32, o16, acc, s);
+    } else if (ng == 2) {
+        if (hz) launch_compute<M, 2, true>(P, o32, o16, acc, s);
+        else launch_compute<M, 2, false>(P, o32, o16, acc, s);
+    } else {
+        if (hz) launch_compute<M, 4, true>(P, o32, o16, acc, s);
+        else launch_compute<M, 4, false>(P, o32, o16, acc, s);
+    }
 }
 
 extern "C" hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table,
@@ -492,6 +650,16 @@ extern "C" hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table
     P.inter = (int)L->rows[0];
     P.gs = (int)L->group_size;
     P.has_zeros = L->has_zeros ? 1 : 0;
+    {
+        const int ngs = P.gs >= 128 ? P.gs : 128;   /* gs * NG */
+        int sh = 0;
+        while ((128 << sh) < ngs) sh++;
+        P.gshift = sh;
+    }
+    P.n_chunks = ((P.inter / 128) + DEC_CHUNK_BLOCKS - 1) / DEC_CHUNK_BLOCKS;
+    P.m_lo = 0x000F000Fu;
+    P.m_hi = 0x00F000F0u;
+    P.one024 = 0x64006400u;
     P.max_u = w.max_u;
     char* ws = (char*)d_workspace;
     P.n_unique = (int*)(ws + w.nu);
@@ -499,6 +667,7 @@ extern "C" hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table
     P.uw = (float*)(ws + w.uw);
     P.xperm = (uint16_t*)(ws + w.xperm);
     P.hperm = (uint16_t*)(ws + w.hperm);
+    P.part = (float*)(ws + w.part);
 
     const int prep_blocks = 1 + (n_tokens * (P.hidden / 8) + 255) / 256;
     ev_before(EV_PREP, s);
@@ -516,13 +685,12 @@ extern "C" hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table
 
     const int gs = P.gs;
     const int ng = gs >= 128 ? 1 : 128 / gs;
-    const int gu_waves = clamp_waves(P.hidden / 128, DEC_GU_MAX_WAVES);
-    const int dn_waves = clamp_waves(w.max_u * (P.inter / 128), DEC_MAX_WAVES);
+    const bool hz = P.has_zeros != 0;
     switch (n_tokens) {
-        case 1: launch_ng<1>(ng, P, gu_waves, dn_waves, d_out_f32, d_out_f16, accumulate, s); break;
-        case 2: launch_ng<2>(ng, P, gu_waves, dn_waves, d_out_f32, d_out_f16, accumulate, s); break;
-        case 3: launch_ng<3>(ng, P, gu_waves, dn_waves, d_out_f32, d_out_f16, accumulate, s); break;
-        default: launch_ng<4>(ng, P, gu_waves, dn_waves, d_out_f32, d_out_f16, accumulate, s); break;
+        case 1: launch_ng<1>(ng, hz, P, d_out_f32, d_out_f16, accumulate, s); break;
+        case 2: launch_ng<2>(ng, hz, P, d_out_f32, d_out_f16, accumulate, s); break;
+        case 3: launch_ng<3>(ng, hz, P, d_out_f32, d_out_f16, accumulate, s); break;
+        default: launch_ng<4>(ng, hz, P, d_out_f32, d_out_f16, accumulate, s); break;
     }
     return hipGetLastError();
 }
