@@ -233,6 +233,26 @@ def measure(layer, steps, warmup):
     }
 
 
+def copy_calibration(mib):
+    """Five launches of a plain copy of `mib` MiB (source and destination
+    both far larger than the Infinity Cache for mib >= 512)."""
+    from wisp_amd import _lib
+    from wisp_amd.hip import DeviceBuffer, synchronize
+    lib = _lib.lib()
+    f = lib.wisp_amd__copy_calibration
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    n = mib << 20
+    src, dst = DeviceBuffer(n), DeviceBuffer(n)
+    src.zero()
+    for _ in range(5):
+        rc = f(dst.ptr, src.ptr, n, None)
+        if rc:
+            raise RuntimeError(f"copy calibration failed: hipError {rc}")
+    synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -240,6 +260,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline workload only")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB 5 times (byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the int4 MoE expert path here is a single-GPU "
@@ -251,6 +273,9 @@ def main():
     if device_count() < 1:
         print("no HIP device visible", file=sys.stderr)
         sys.exit(1)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
 
     # 4 Mixtral expert sets (3 GB) so consecutive steps stream cold weights
     head = Layer(synth.MIXTRAL, 1, seed=1234, n_sets=4)

@@ -210,3 +210,23 @@ extern "C" void wisp_gpu_scale_accum(float* acc, const float* x, float w, int n,
     hipLaunchKernelGGL(scale_accum_kernel, dim3((n + 255) / 256), dim3(256), 0, s,
                        acc, x, w, n);
 }
+
+/* Plain 16-byte-per-lane copy of a known byte count. Not part of the
+ * reference interface: hardware byte counters (FETCH_SIZE / WRITE_SIZE)
+ * read over this kernel give the factor that turns their units into bytes
+ * moved. Requires 16-byte aligned pointers and bytes % 16 == 0. */
+__global__ void copy_calibration_kernel(uint4* __restrict__ dst, const uint4* __restrict__ src,
+                                        size_t n16) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16; i += stride)
+        dst[i] = src[i];
+}
+
+extern "C" hipError_t wisp_amd__copy_calibration(void* dst, const void* src, size_t bytes,
+                                                 hipStream_t s) {
+    if (bytes == 0 || bytes % 16 || (uintptr_t)dst % 16 || (uintptr_t)src % 16)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(copy_calibration_kernel, dim3(4096), dim3(256), 0, s, (uint4*)dst,
+                       (const uint4*)src, bytes / 16);
+    return hipGetLastError();
+}
