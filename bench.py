@@ -4,8 +4,11 @@ Headline workload: one Mixtral-8x7B-shape MoE layer decode, M = 1 token:
 router GEMV + softmax top-2 on the device, then the fused int4 expert FFN
 (gate/up/SiLU, down, weighted combine) over the 2 routed experts; 8 experts
 of hidden 4096 / inter 14336, int4 g128, fp16 scales, all resident in HBM.
-One step = one MoE layer on one fixed synthetic token; `value` is the mean
-microseconds per layer over the timed steps (lower is better).
+One step = one MoE layer on one synthetic token (one library call:
+wisp_gpu_moe_layer_decode_int4). `value` is the mean device microseconds per
+layer over K consecutive layers replayed from one HIP graph (how a serving
+loop issues a decode step); the eager, Python-launched figure is reported
+beside it (lower is better for both).
 
 Also reported (same JSON line, "extra"): Mixtral M=4 and DeepSeek-V3-shape
 decode (256 routed experts + 1 shared, inter 2048, hidden 7168, sigmoid
@@ -92,14 +95,19 @@ class Layer:
         return self.dx.ptr + (i % self.n_pool) * self.M * self.shape.hidden * 2
 
     def step(self, i):
+        """One MoE layer: router + top-k + experts in one library call."""
         from wisp_amd import moe
         s = self.shape
         a = self.arenas[i % len(self.arenas)]
-        moe.moe_route(self.dW.ptr, 0, self.xptr(i), self.M, s.hidden, s.n_experts, s.top_k,
-                      self.kind, self.logits.ptr, self.idx.ptr, self.w.ptr, self.stream.handle)
-        moe.moe_decode_int4(a.table.ptr, self.shared_dev.ptr + 8 if s.shared else 0, a.layout,
-                            self.xptr(i), self.M, self.idx.ptr, self.w.ptr, s.top_k, s.n_experts,
-                            self.ws, self.out32.ptr, self.out16.ptr, self.stream.handle)
+        moe.moe_layer_decode_int4(self.dW.ptr, 0, self.kind, self.logits.ptr, self.idx.ptr,
+                                  self.w.ptr, a.table.ptr,
+                                  self.shared_dev.ptr + 8 if s.shared else 0, a.layout,
+                                  self.xptr(i), self.M, s.top_k, s.n_experts, self.ws,
+                                  self.out32.ptr, self.out16.ptr, self.stream.handle)
+
+    def separate_router(self):
+        """True when the router GEMV gets its own launch (matrix > 256 KiB)."""
+        return self.shape.n_experts * self.shape.hidden * 2 > 256 * 1024
 
     def token_bytes(self):
         """Per pool token: algorithmic HBM bytes (packed + scales; zeros are
@@ -128,8 +136,12 @@ class Layer:
 
 
 def time_layer(layer, steps, warmup):
+    """Device time per layer over `steps` consecutive layers, two ways:
+    replayed from one HIP graph holding all of them (no host launch cost:
+    how a serving loop runs a decode step) and launched eagerly from
+    Python; then the per-kernel durations from events around each kernel."""
     from wisp_amd import _lib
-    from wisp_amd.hip import Event, synchronize
+    from wisp_amd.hip import Event, Graph, synchronize
     for i in range(warmup):
         layer.step(i)
     synchronize()
@@ -141,7 +153,16 @@ def time_layer(layer, steps, warmup):
     e1.record(layer.stream.handle)
     synchronize()
     host_ms = (time.perf_counter() - t0) * 1e3
+    eager_ms = e0.elapsed_ms(e1)
+    graph = Graph(layer.stream, lambda: [layer.step(i) for i in range(steps)])
+    graph.launch(layer.stream)       # warm replay
+    synchronize()
+    e0.record(layer.stream.handle)
+    graph.launch(layer.stream)
+    e1.record(layer.stream.handle)
+    synchronize()
     dev_ms = e0.elapsed_ms(e1)
+    del graph
     # per-kernel durations: same steps again with events around each kernel
     evs = [[Event() for _ in range(2 * EV_KINDS)] for _ in range(steps)]
     arrs = [(ctypes.c_void_p * (2 * EV_KINDS))(*[e.handle for e in row]) for row in evs]
@@ -152,11 +173,13 @@ def time_layer(layer, steps, warmup):
     lib.wisp_amd_set_kernel_events(None, 0)
     synchronize()
     kern = {}
-    for name, k in (("route", EV_ROUTE), ("prep", EV_PREP), ("gate_up", EV_GATEUP), ("down", EV_DOWN),
-                    ("combine", EV_COMBINE)):
+    kinds = (("prep", EV_PREP), ("gate_up", EV_GATEUP), ("down", EV_DOWN), ("combine", EV_COMBINE))
+    if layer.separate_router():
+        kinds = (("router_gemv", EV_ROUTE),) + kinds
+    for name, k in kinds:
         kern[name] = 1e3 * float(np.mean([evs[i][2 * k].elapsed_ms(evs[i][2 * k + 1]) for i in range(steps)]))
-    return {"us_per_layer": 1e3 * dev_ms / steps, "host_us_per_layer": 1e3 * host_ms / steps,
-            "kernel_us": kern}
+    return {"us_per_layer": 1e3 * dev_ms / steps, "eager_us_per_layer": 1e3 * eager_ms / steps,
+            "host_us_per_layer": 1e3 * host_ms / steps, "kernel_us": kern}
 
 
 def cpu_baseline(layer, budget_s=10.0):
@@ -224,6 +247,8 @@ def measure(layer, steps, warmup):
     us = r["us_per_layer"]
     return {
         "us_per_layer": round(us, 3),
+        "eager_us_per_layer": round(r["eager_us_per_layer"], 3),
+        "host_us_per_layer": round(r["host_us_per_layer"], 3),
         "layer_hbm_frac": round(b["layer"] / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "n_unique_experts": round(b["n_unique"], 2),
         "kernel_us": {k: round(v, 3) for k, v in r["kernel_us"].items()},

@@ -192,12 +192,13 @@ hipError_t wisp_gpu_moe_scatter(const float* d_y, const int* d_inv,
  *    out[t] = shared(x_t) + sum_k w[t,k] * expert_{idx[t,k]}(x_t)
  *    expert(x) = down . (silu(gate . x) * (up . x))
  *
- *    A small prep kernel, then (a) gate+up+SiLU over every unique expert
- *    touched by the M tokens in one launch, (b) the down projections of all
- *    of them in one launch, (c) a fixed-order combine of the per-expert
- *    outputs (routing weights are folded in before the down projection).
- *    Weights stream from the blobs in place; nothing is dequantised to
- *    memory. Routing stays on the device.
+ *    A one-workgroup prep kernel (unique-expert list, routing weights),
+ *    then (a) gate+up+SiLU over every unique expert touched by the M tokens
+ *    in one launch, (b) the down projections of all of them in one launch,
+ *    (c) a fixed-order combine of the per-expert partials (routing weights
+ *    are folded in before the down projection). Weights stream from the
+ *    blobs in place; nothing is dequantised to memory. Routing stays on
+ *    the device.
  * ======================================================================= */
 
 enum { WISP_DTYPE_F16 = 0, WISP_DTYPE_F32 = 1 };
@@ -227,13 +228,39 @@ hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table,
                                     float* d_out_f32, wisp_half* d_out_f16,
                                     hipStream_t s);
 
+/* One MoE layer for M = 1..4 tokens, routing included, with no host round
+ * trip: router logits = W x (+ bias), softmax or sigmoid top-k with the
+ * rules of wisp_gpu_moe_route, then everything wisp_gpu_moe_decode_int4
+ * does. The router GEMV runs inside the prep kernel when W is at most
+ * 256 KiB (4 launches per layer), else in one launch before it. Writes the
+ * post-activation scores [n_tokens, n_experts] to d_scores and the
+ * selection [n_tokens, top_k] to d_topk_idx / d_topk_w (device), as
+ * wisp_gpu_moe_route does. Workspace: wisp_moe_decode_workspace_bytes.
+ * Replaces the routed-expert part of run_moe for VRAM-resident experts
+ * (csrc/core/wisp_engine.c:1563-1674: router launch, host sync at :1576,
+ * then the per-expert gpu_expert_ffn loop at :1653-1670). */
+hipError_t wisp_gpu_moe_layer_decode_int4(const wisp_half* d_router_w,
+                                          const wisp_half* d_router_bias,
+                                          int router_kind, float* d_scores,
+                                          int* d_topk_idx, float* d_topk_w,
+                                          const void* const* d_expert_table,
+                                          const void* d_shared_blob,
+                                          const WispExpertLayout* L,
+                                          const void* d_x, int x_dtype,
+                                          int n_tokens, int top_k,
+                                          int n_experts, void* d_workspace,
+                                          size_t workspace_bytes,
+                                          int accumulate, float* d_out_f32,
+                                          wisp_half* d_out_f16, hipStream_t s);
+
 /* ======================================================================= *
  * 9. Profiling hook
  * ======================================================================= */
 
 /* When events != NULL, the fused launchers record events[2*k] before and
  * events[2*k+1] after each kernel of kind k < n_pairs on the launch stream:
- * k = 0 router (wisp_gpu_moe_route), 1 decode prep, 2 decode gate/up,
+ * k = 0 router (wisp_gpu_moe_route, or the router GEMV launch of
+ * wisp_gpu_moe_layer_decode_int4), 1 decode prep, 2 decode gate/up,
  * 3 decode down, 4 decode combine, 5 prefill gate/up, 6 prefill down. Process-wide; for
  * timing runs only; not thread-safe. */
 void wisp_amd_set_kernel_events(hipEvent_t* events, int n_pairs);

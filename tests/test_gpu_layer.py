@@ -1,0 +1,160 @@
+"""GPU parity of the one-call MoE layer decode (wisp_gpu_moe_layer_decode_int4:
+router + top-k + shared/routed experts, no host round trip) against the CPU
+oracle: routing indices must equal the oracle's wherever the top-k is not
+decided by a near-tie of the logits, and the layer output must meet the
+fp16 bar of tests/gpu_util.py (max-rel-err <= 1e-2, cosine >= 0.9999).
+
+Also: the result is bit-identical across repeated calls on one workspace
+(the down kernel's row-tile counters reset each call and the final sum runs
+in a fixed order), and a layer with nothing routed writes zeros."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.gpu_util import assert_close, make_expert
+from wisp_amd import moe, synth
+from wisp_amd.hip import DeviceBuffer, synchronize, to_device
+
+pytestmark = pytest.mark.gpu
+
+
+def _keys(W, x, bias, kind):
+    """float64 selection keys of one token."""
+    l = W.astype(np.float64) @ x.astype(np.float64)
+    b = bias.astype(np.float64) if bias is not None else 0.0
+    return l + b if kind == "softmax" else 1.0 / (1.0 + np.exp(-l)) + b
+
+
+def _near_tie(W, x, bias, kind, k):
+    """True when two of the k+1 largest selection keys are too close for the
+    selection to be decided by fp32 summation order (the logits' fp32 error
+    is ~1e-7 here; 2e-5 leaves a wide margin)."""
+    key = _keys(W, x, bias, kind)
+    srt = np.sort(key)[::-1]
+    return np.min(np.abs(np.diff(srt[: k + 1]))) <= 2e-5 * max(np.max(np.abs(key)), 1.0)
+
+
+def run_layer(seed, inter, hidden, n_exp, top_k, M, kind, shared, use_bias, repeat=1,
+              gs=128, zeros=False):
+    rng = np.random.default_rng(seed)
+    W = synth.make_router(rng, n_exp, hidden, std=0.05)
+    bias = (rng.standard_normal(n_exp) * 0.1).astype(np.float16) if use_bias else None
+    x = synth.make_x(rng, M, hidden)
+    # upload only the experts the routing can reach: each token's k + 4 best
+    # keys (the slots of the others are never read)
+    cand = sorted({int(e) for t in range(M)
+                   for e in np.argsort(-_keys(W, x[t], bias, kind))[: top_k + 4]})
+    arena = moe.ExpertArena(n_exp, inter, hidden, gs,
+                            lambda e, out: make_expert(seed, e, inter, hidden, gs, zeros, out),
+                            has_zeros=zeros, keep_host=cand, only=cand)
+    sh_blob = make_expert(seed, 10_000, inter, hidden, gs, zeros) if shared else None
+    sh_dev = None
+    if shared:
+        sh_dev = DeviceBuffer(sh_blob.nbytes + 16)
+        sh_dev.upload(sh_blob, offset=8)
+    dW, dx = to_device(W), to_device(x)
+    db = to_device(bias) if use_bias else None
+    sc, di, dw = DeviceBuffer(4 * M * n_exp), DeviceBuffer(4 * M * top_k), DeviceBuffer(4 * M * top_k)
+    ws = DeviceBuffer(moe.decode_workspace_bytes(arena.layout, M, top_k, shared))
+    out32, out16 = DeviceBuffer(4 * M * hidden), DeviceBuffer(2 * M * hidden)
+    kcode = moe.ROUTER_SOFTMAX if kind == "softmax" else moe.ROUTER_SIGMOID
+    results = []
+    for _ in range(repeat):
+        moe.moe_layer_decode_int4(dW.ptr, db.ptr if use_bias else 0, kcode, sc.ptr, di.ptr, dw.ptr,
+                                  arena.table.ptr, sh_dev.ptr + 8 if shared else 0, arena.layout,
+                                  dx.ptr, M, top_k, n_exp, ws, out32.ptr, out16.ptr)
+        synchronize()
+        results.append(out32.download(np.float32, (M, hidden)))
+    g32 = results[-1]
+    g16 = out16.download(np.float16, (M, hidden)).astype(np.float32)
+    gi = di.download(np.int32, (M, top_k))
+    gw = dw.download(np.float32, (M, top_k))
+    blobs = [arena.host.get(e, arena.host[cand[0]]) for e in range(n_exp)]
+    checked = 0
+    for t in range(M):
+        oi, ow, _ = O.router_topk(W.view(np.uint16), bias.view(np.uint16) if use_bias else None,
+                                  x[t].astype(np.float32), top_k, kind=kind)
+        if _near_tie(W, x[t], bias, kind, top_k):
+            # selection decided by rounding: check the experts' math on the
+            # device's own selection instead
+            assert set(gi[t].tolist()) <= set(cand)
+            oi, ow = gi[t], gw[t]
+        else:
+            assert set(oi.tolist()) <= set(cand)
+            assert gi[t].tolist() == oi.tolist(), (t, gi[t], oi)
+            assert np.allclose(gw[t], ow, rtol=1e-4, atol=1e-6), (t, gw[t], ow)
+        want = O.moe_combine(blobs, sh_blob, x[t].astype(np.float32), oi, ow)
+        assert_close(g32[t], want, f"token {t} fp32")
+        assert_close(g16[t], want, f"token {t} fp16")
+        checked += 1
+    assert checked == M
+    for r in results[:-1]:
+        assert np.array_equal(r, g32), "repeated calls differ"
+    return g32
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_fused_router_softmax(M):
+    print(f"layer softmax fused-router M={M}", flush=True)
+    run_layer(500 + M, 256, 512, 8, 2, M, "softmax", shared=(M % 2 == 0), use_bias=(M > 2))
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_fused_router_sigmoid_bias(M):
+    print(f"layer sigmoid fused-router M={M}", flush=True)
+    run_layer(600 + M, 256, 512, 32, 4, M, "sigmoid", shared=True, use_bias=True)
+
+
+@pytest.mark.parametrize("kind", ["softmax", "sigmoid"])
+def test_separate_router_launch(kind):
+    # 256 experts x 1024 hidden x 2 B = 512 KiB router: logits in their own launch
+    print(f"layer {kind} separate-router", flush=True)
+    run_layer(700, 256, 1024, 256, 8, 3, kind, shared=True, use_bias=(kind == "sigmoid"))
+
+
+def test_repeated_calls_bit_identical_with_zeros():
+    print("layer repeat x3", flush=True)
+    run_layer(800, 384, 640, 16, 4, 2, "softmax", shared=True, use_bias=False, repeat=3,
+              zeros=True)
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_mixtral_layer(M):
+    print(f"layer mixtral M={M}", flush=True)
+    s = synth.MIXTRAL
+    run_layer(900 + M, s.inter, s.hidden, s.n_experts, s.top_k, M, "softmax", shared=False,
+              use_bias=False, repeat=2)
+
+
+def test_dsv3_layer_m1():
+    print("layer dsv3 M=1", flush=True)
+    s = synth.DSV3
+    run_layer(950, s.inter, s.hidden, s.n_experts, s.top_k, 1, "sigmoid", shared=True,
+              use_bias=False)
+
+
+def test_nothing_routed_writes_zeros():
+    print("decode nothing routed", flush=True)
+    rng = np.random.default_rng(11)
+    inter, hidden, n_exp, k, M = 256, 512, 8, 2, 2
+    arena = moe.ExpertArena(n_exp, inter, hidden, 128,
+                            lambda e, out: make_expert(11, e, inter, hidden, 128, False, out),
+                            has_zeros=False, only=[0])
+    x = synth.make_x(rng, M, hidden)
+    dx = to_device(x)
+    di = to_device(np.full((M, k), -1, np.int32))
+    dw = to_device(np.full((M, k), 0.5, np.float32))
+    ws = DeviceBuffer(moe.decode_workspace_bytes(arena.layout, M, k, False))
+    out32, out16 = DeviceBuffer(4 * M * hidden), DeviceBuffer(2 * M * hidden)
+    out32.upload(np.full((M, hidden), 7.0, np.float32))
+    moe.moe_decode_int4(arena.table.ptr, 0, arena.layout, dx.ptr, M, di.ptr, dw.ptr, k, n_exp, ws,
+                        out32.ptr, out16.ptr)
+    synchronize()
+    assert np.all(out32.download(np.float32, (M, hidden)) == 0.0)
+    assert np.all(out16.download(np.float16, (M, hidden)) == 0.0)
+    base = np.full((M, hidden), 3.5, np.float32)
+    out32.upload(base)
+    moe.moe_decode_int4(arena.table.ptr, 0, arena.layout, dx.ptr, M, di.ptr, dw.ptr, k, n_exp, ws,
+                        out32.ptr, 0, accumulate=True)
+    synchronize()
+    assert np.array_equal(out32.download(np.float32, (M, hidden)), base)

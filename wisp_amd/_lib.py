@@ -49,6 +49,9 @@ _SIGS = {
     "wisp_moe_decode_workspace_bytes": (c_size_t, [POINTER(WispExpertLayout), c_int, c_int, c_int]),
     "wisp_gpu_moe_decode_int4": (c_int, [P, P, POINTER(WispExpertLayout), P, c_int, c_int, P, P,
                                          c_int, c_int, P, c_size_t, c_int, P, P, P]),
+    "wisp_gpu_moe_layer_decode_int4": (c_int, [P, P, c_int, P, P, P, P, P, POINTER(WispExpertLayout),
+                                               P, c_int, c_int, c_int, c_int, P, c_size_t, c_int,
+                                               P, P, P]),
     # profiling
     "wisp_amd_set_kernel_events": (None, [P, c_int]),
     "wisp_amd_version": (c_char_p, []),

@@ -2,41 +2,52 @@
  * moe_decode.hip — fused int4 MoE decode for M = 1..4 tokens on gfx950.
  *
  * Replaces the reference's per-expert chain (csrc/core/wisp_engine.c:
- * 1507-1531 and 1563-1674: 3 full-matrix dequants into fp16 scratch, a
- * fused gate/up GEMV, a down GEMV and a scale-accumulate, per expert) with
- * three launches per MoE layer:
+ * 1507-1531 and 1563-1674: a router launch and a host round trip, then per
+ * expert 3 full-matrix dequants into fp16 scratch, a fused gate/up GEMV, a
+ * down GEMV and a scale-accumulate) with three launches per MoE layer:
  *
- *   prep    : unique-expert list of the M tokens (shared expert first, then
- *             first appearance in flat (token, slot) order), per-(expert,
- *             token) routing weights, and x permuted into the MFMA operand
- *             order of unpack8_magic.
- *   gate/up : grid (inter/32 row blocks) x (unique experts). Each wave owns a
+ *   prep    : one workgroup. Optionally the router itself (logits, softmax
+ *             or sigmoid top-k; the GEMV runs here when the router matrix is
+ *             small, else in router_logits_kernel just before), then the
+ *             unique-expert list of the M tokens (shared expert first, then
+ *             first appearance in flat (token, slot) order) with per-(expert,
+ *             token) routing weights, and the reset of the down kernel's
+ *             row-tile counters.
+ *   gate/up : grid (inter/16 row tiles) x (unique experts). Each wave owns a
  *             K range; per 128-element block it loads 16 B of packed nibbles
- *             per lane for 2 gate + 2 up row tiles (a lane's 16 B are 32
+ *             per lane for one gate and one up row tile (a lane's 16 B are 32
  *             consecutive elements of one row), unpacks them with 5 integer
  *             ops per 8 values and feeds v_mfma_f32_16x16x32_f16 with the
  *             activations as the A operand (M of its 16 rows used) and the
  *             weights as B. One extra MFMA per block against a constant
  *             operand yields the magic-number excess (a second one sum(x)
  *             when zero points are present); the group scale and zero are
- *             applied per block in fp32. The K split is
+ *             applied per block in fp32. The activations are permuted into
+ *             the operand order while they are staged in LDS. The K split is
  *             reduced through LDS in a fixed order; the epilogue writes
  *             h' = w_route * silu(g) * u in fp16, already permuted for the
  *             down kernel.
- *   down    : grid (hidden/16 row blocks). The K range of a block is the
- *             concatenation of all unique experts' inter dimensions, so the
- *             routed sum happens inside the contraction; routing weights are
- *             folded into h'. Output fp32 and/or fp16.
+ *   down    : grid (hidden/16 row tiles) x (unique experts x K chunks of
+ *             4096). Each workgroup writes its partial sums (routing weights
+ *             are already folded into h').
+ *   combine : adds the partials in a fixed order (shared expert, then
+ *             routed experts in unique-list order, then K chunk), so the
+ *             result is deterministic. A separate launch on purpose: a
+ *             device-scope fence inside the down kernel costs an L2
+ *             write-back per wave on this part, far more than a launch.
  *
  * Weights are read once, in place, from the reference blob layout
  * (csrc/core/wisp_engine.h:214-238); nothing is dequantised to memory.
  */
-#include "hip_common.h"
+#include "route_common.h"
 
 #define DEC_MAX_TOKENS 4
 #define DEC_MAX_TOPK 64
 #define DEC_MAX_WAVES 8
 #define DEC_CHUNK_BLOCKS 32   /* down-projection K chunk per workgroup: 4096 elements */
+#define DEC_ROUTE_FUSE_BYTES (256 * 1024)   /* router matrices up to this size run in prep */
+#define DEC_ROUTE_MAX_EXPERTS 1024
+#define DEC_PREP_THREADS 512
 
 struct DecodeParams {
     uint64_t p_off[3], s_off[3], z_off[3];
@@ -45,105 +56,138 @@ struct DecodeParams {
     int n_chunks;         /* down-projection K chunks: ceil(inter/128 / DEC_CHUNK_BLOCKS) */
     uint32_t m_lo, m_hi, one024;  /* unpack masks 0x000F000F, 0x00F000F0, 0x64006400 */
     int max_u;
+    int M;
     int* n_unique;
     const uint8_t** ublob;
     float* uw;            /* [max_u][4] routing weight of each token     */
-    uint16_t* xperm;      /* [M][hidden] permuted fp16 activations        */
+    const uint16_t* xh;   /* [M][hidden] fp16 activations (caller's or a converted copy) */
+    uint16_t* xconv;      /* workspace copy used when the caller's x is fp32 or unaligned */
     uint16_t* hperm;      /* [max_u][M][inter] permuted fp16 h'           */
     float* part;          /* [max_u][n_chunks][M][hidden] down partials   */
+    float* out32;         /* [M][hidden] layer output (either may be null) */
+    uint16_t* out16;
+    int accumulate;
+};
+
+/* Routing inputs of the prep kernel. mode 0: idx/w are given; mode 1: raw
+ * logits [M][n_experts] were written to `logits` by router_logits_kernel;
+ * mode 2: the router GEMV runs inside prep. In modes 1 and 2 `logits`
+ * receives the post-activation scores and idx/w the selection. */
+struct RouteArgs {
+    const uint16_t* W;
+    const uint16_t* bias;
+    int kind, mode;
+    float* logits;
+    int* idx;
+    float* w;
 };
 
 /* ======================================================================= */
 /* prep                                                                     */
 /* ======================================================================= */
 
-template <typename XT>
-__device__ __forceinline__ float load_x(const XT* x, size_t i);
-template <> __device__ __forceinline__ float load_x<float>(const float* x, size_t i) { return x[i]; }
-template <> __device__ __forceinline__ float load_x<uint16_t>(const uint16_t* x, size_t i) {
-    return half_bits_to_float(x[i]);
-}
+__host__ __device__ constexpr int align_up_dev(int v, int a) { return (v + a - 1) / a * a; }
 
-/* Writes one 8-element block of a permuted activation row: even elements
- * as fp16(v), odd elements as fp16(v / 16), in unpack8_magic slot order. */
-__device__ __forceinline__ void store_perm8(uint16_t* dst, const float* v) {
-    uint16_t o[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        f16 h = (f16)((e & 1) ? v[e] * 0.0625f : v[e]);
-        o[perm_slot(e)] = __builtin_bit_cast(uint16_t, h);
+/* One workgroup of DEC_PREP_THREADS. Every global load it needs (the expert
+ * table, and in mode 2 each wave's first router row and the token rows) is
+ * issued before the first barrier, so the kernel costs about one memory
+ * round trip. */
+template <typename XT>
+__global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
+    DecodeParams P, RouteArgs R, const void* const* __restrict__ table, const void* shared_blob,
+    const XT* __restrict__ x, int top_k, int n_experts) {
+    constexpr int NWV = DEC_PREP_THREADS / 64;
+    __shared__ int s_e[DEC_MAX_TOKENS * DEC_MAX_TOPK];
+    __shared__ float s_w[DEC_MAX_TOKENS * DEC_MAX_TOPK];
+    __shared__ int s_wcount[NWV];
+    __shared__ const uint8_t* s_tab[DEC_ROUTE_MAX_EXPERTS];
+    const int M = P.M;
+    const int n_pairs = M * top_k;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+
+    for (int e = threadIdx.x; e < n_experts; e += blockDim.x) s_tab[e] = (const uint8_t*)table[e];
+    /* x -> fp16 copy when the gate/up kernel cannot read the caller's x */
+    if (P.xconv) {
+        for (int i = threadIdx.x; i < M * P.hidden; i += blockDim.x)
+            P.xconv[i] = __builtin_bit_cast(uint16_t, (f16)xval<XT>(x, i));
     }
-    u4 q;
-    q.x = o[0] | ((uint32_t)o[1] << 16);
-    q.y = o[2] | ((uint32_t)o[3] << 16);
-    q.z = o[4] | ((uint32_t)o[5] << 16);
-    q.w = o[6] | ((uint32_t)o[7] << 16);
-    *(u4*)dst = q;
-}
 
-template <typename XT>
-__global__ __launch_bounds__(256) void decode_prep_kernel(DecodeParams P,
-                                                          const void* const* __restrict__ table,
-                                                          const void* shared_blob,
-                                                          const XT* __restrict__ x, int M,
-                                                          const int* __restrict__ idx,
-                                                          const float* __restrict__ w,
-                                                          int top_k, int n_experts) {
-    if (blockIdx.x == 0) {
-        /* unique list: one thread per (token, slot) pair, <= 256 pairs */
-        __shared__ int s_e[DEC_MAX_TOKENS * DEC_MAX_TOPK];
-        __shared__ int s_wcount[4];
-        const int n_pairs = M * top_k;
-        const int p = threadIdx.x;
-        const int lane = p & 63, wv = p >> 6;
-        const int base = shared_blob ? 1 : 0;
-        int e = -1;
-        if (p < n_pairs) {
-            e = idx[p];
-            if (e < 0 || e >= n_experts) e = -1;
-            s_e[p] = e;
-        }
-        __syncthreads();
-        int first_p = -1;
-        if (e >= 0) {
-            for (int q = 0; q < p; q++)
-                if (s_e[q] == e) { first_p = q; break; }
-        }
-        const bool is_first = (e >= 0 && first_p < 0);
-        uint64_t m = __ballot(is_first);
-        if (lane == 0) s_wcount[wv] = __popcll(m);
-        __syncthreads();
-        int before = base;
-        for (int q = 0; q < wv; q++) before += s_wcount[q];
-        if (is_first) {
-            int slot = before + __popcll(m & ((1ull << lane) - 1ull));
-            P.ublob[slot] = (const uint8_t*)table[e];
-            /* weights of every token for this expert, in flat pair order */
-            float acc[DEC_MAX_TOKENS] = {0.f, 0.f, 0.f, 0.f};
-            for (int q = p; q < n_pairs; q++)
-                if (s_e[q] == e) acc[q / top_k] += w[q];
-            for (int v = 0; v < DEC_MAX_TOKENS; v++) P.uw[slot * 4 + v] = acc[v];
-        }
-        if (p == 0) {
-            int total = base;
-            for (int q = 0; q < 4; q++) total += (q * 64 < n_pairs) ? s_wcount[q] : 0;
-            *P.n_unique = total;
-            if (shared_blob) {
-                P.ublob[0] = (const uint8_t*)shared_blob;
-                for (int v = 0; v < DEC_MAX_TOKENS; v++) P.uw[v] = v < M ? 1.0f : 0.0f;
+    if (R.mode != 0) {
+        /* dynamic LDS: selection keys [M][n_experts], scores [M][n_experts]
+         * (the raw logits first, in mode 2), then x [M][hidden] (mode 2) */
+        extern __shared__ __attribute__((aligned(16))) uint8_t lds_raw[];
+        float* s_key = (float*)lds_raw;
+        float* s_sc = s_key + M * n_experts;
+        if (R.mode == 2) {
+            XT* s_x = (XT*)(lds_raw + align_up_dev(2 * M * n_experts * 4, 16));
+            u4 wrow[ROUTE_UNROLL];
+            if (wv < n_experts) router_row_load(R.W + (size_t)wv * P.hidden, P.hidden, lane, wrow);
+            stage_rows<XT>(s_x, x, M, P.hidden);
+            __syncthreads();
+            const uint16_t* bias = R.kind == WISP_ROUTER_SOFTMAX ? R.bias : nullptr;
+            for (int e = wv; e < n_experts; e += NWV) {
+                if (e != wv) router_row_load(R.W + (size_t)e * P.hidden, P.hidden, lane, wrow);
+                router_row_fma<XT>(wrow, s_x, M, P.hidden, lane, s_sc + e, n_experts,
+                                   bias ? half_bits_to_float(bias[e]) : 0.0f);
             }
+            __syncthreads();
         }
-        return;
+        if (wv < M) {
+            const float* lg = R.mode == 2 ? s_sc + wv * n_experts : R.logits + (size_t)wv * n_experts;
+            topk_lds(lg, R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr, s_key + wv * n_experts,
+                     s_sc + wv * n_experts, R.logits + (size_t)wv * n_experts, n_experts, top_k,
+                     R.kind, s_e + wv * top_k, s_w + wv * top_k, lane);
+        }
+    } else {
+        for (int p = threadIdx.x; p < n_pairs; p += blockDim.x) {
+            s_e[p] = R.idx[p];
+            s_w[p] = R.w[p];
+        }
     }
-    /* permuted activations: one 8-element block per thread */
-    const int nb = M * (P.hidden / 8);
-    for (int i = (blockIdx.x - 1) * blockDim.x + threadIdx.x; i < nb;
-         i += (gridDim.x - 1) * blockDim.x) {
-        const int v = i / (P.hidden / 8), b = i - v * (P.hidden / 8);
-        float xv[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) xv[e] = load_x<XT>(x, (size_t)v * P.hidden + b * 8 + e);
-        store_perm8(P.xperm + (size_t)v * P.hidden + b * 8, xv);
+    __syncthreads();
+    if (R.mode != 0) {
+        for (int p = threadIdx.x; p < n_pairs; p += blockDim.x) {
+            R.idx[p] = s_e[p];
+            R.w[p] = s_w[p];
+        }
+    }
+
+    /* unique list: one thread per (token, slot) pair, <= 256 pairs */
+    const int base = shared_blob ? 1 : 0;
+    const int p = threadIdx.x;
+    int e = -1;
+    if (p < n_pairs) {
+        e = s_e[p];
+        if (e < 0 || e >= n_experts) e = -1;
+    }
+    int first_p = -1;
+    if (e >= 0) {
+        for (int q = 0; q < p; q++)
+            if (s_e[q] == e) { first_p = q; break; }
+    }
+    const bool is_first = (e >= 0 && first_p < 0);
+    const uint64_t m = __ballot(is_first);
+    if (lane == 0) s_wcount[wv] = __popcll(m);
+    __syncthreads();
+    int before = base;
+    for (int q = 0; q < wv; q++) before += s_wcount[q];
+    if (is_first) {
+        const int slot = before + __popcll(m & ((1ull << lane) - 1ull));
+        P.ublob[slot] = s_tab[e];
+        /* weights of every token for this expert, in flat pair order */
+        float acc[DEC_MAX_TOKENS] = {0.f, 0.f, 0.f, 0.f};
+        for (int q = p; q < n_pairs; q++)
+            if (s_e[q] == e) acc[q / top_k] += s_w[q];
+        for (int v = 0; v < DEC_MAX_TOKENS; v++) P.uw[slot * 4 + v] = acc[v];
+    }
+    if (p == 0) {
+        int total = base;
+        for (int q = 0; q < NWV; q++) total += s_wcount[q];
+        *P.n_unique = total;
+        if (shared_blob) {
+            P.ublob[0] = (const uint8_t*)shared_blob;
+            for (int v = 0; v < DEC_MAX_TOKENS; v++) P.uw[v] = v < M ? 1.0f : 0.0f;
+        }
     }
 }
 
@@ -256,23 +300,85 @@ __device__ __forceinline__ void stage_groups(uint16_t* dst, const uint16_t* tab,
     }
 }
 
-/* Streams blocks [b0, b1) (absolute block indices of the weight rows) of NT
- * row tiles into tot, in batches of PF blocks: the weight loads of a whole
- * batch are issued first, then the batch is computed. No load result is
- * carried across loop iterations, so the compiler never has to copy (and
- * therefore wait on) an in-flight register; latency is covered by the other
- * resident waves. Activations and scales come from the LDS image, whose K
- * range starts at block xb0 and whose groups start at g_lo. The last batch
- * clamps its loads to the last block (the repeats hit in cache) and
- * computes its padding slots with zero scale. */
-template <int M, int NG, int NT, int PF, bool HZ>
-__device__ __forceinline__ void stream_blocks(const uint8_t* const (&wp)[NT], const uint8_t* smem,
-                                              const LdsMap& L, int b0, int b1, int xb0, int g_lo,
-                                              int gshift, int col, int j, uint32_t m_lo,
-                                              uint32_t m_hi, uint32_t one024,
-                                              float (&tot)[NT][M]) {
-    constexpr int B = PF;
-    if (b0 >= b1) return;
+/* A cooperative global -> LDS copy in two phases, so that its loads can be
+ * issued before a wave's weight loads: loads return in order, so anything
+ * issued after the weights would wait for all of them. The copy is `rows`
+ * rows of `w16` 16-byte pieces; piece q of row r comes from
+ * src + r * src_stride + 16 q and goes to dst + r * dst_stride + 16 q. Each
+ * thread handles at most CNT pieces (ok() tells whether the copy fits);
+ * out-of-range slots load a clamped in-range piece and store nothing. */
+template <int CNT>
+struct Stage16 {
+    u4 v[CNT];
+    int rows, w16;
+
+    __device__ static bool ok(int rows_, int w16_) {
+        return rows_ * w16_ <= CNT * (int)blockDim.x;
+    }
+    __device__ __forceinline__ void issue(const uint8_t* src, size_t src_stride, int rows_,
+                                          int w16_) {
+        rows = rows_;
+        w16 = w16_;
+        const int total = rows * w16;
+#pragma unroll
+        for (int c = 0; c < CNT; c++) {
+            const int i = min((int)threadIdx.x + c * (int)blockDim.x, total - 1);
+            const int r = i / w16, q = i - r * w16;
+            v[c] = *(const u4*)(src + r * src_stride + 16 * q);
+        }
+    }
+    /* perm: permute each piece (8 fp16) into unpack8_magic slot order with
+     * odd elements divided by 16 (exact: a power-of-two scale). */
+    template <bool PERM>
+    __device__ __forceinline__ void commit(uint8_t* dst, int dst_stride) const {
+        const int total = rows * w16;
+        const f16 sixteenth = (f16)0.0625f;
+#pragma unroll
+        for (int c = 0; c < CNT; c++) {
+            const int i = (int)threadIdx.x + c * (int)blockDim.x;
+            if (i < total) {
+                const int r = i / w16, q = i - r * w16;
+                u4 o = v[c];
+                if (PERM) {
+                    const h8 in = __builtin_bit_cast(h8, v[c]);
+                    h8 pv;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) pv[perm_slot(e)] = (e & 1) ? in[e] * sixteenth : in[e];
+                    o = __builtin_bit_cast(u4, pv);
+                }
+                *(u4*)(dst + r * dst_stride + 16 * q) = o;
+            }
+        }
+    }
+};
+
+/* Issues the weight loads of the NB blocks b_first .. b_first + NB - 1 of NT
+ * row tiles (absolute block indices, each clamped to b_clamp so that every
+ * address is in the matrix). A wave issues all of them before anything
+ * else: fully unrolled, so no load result is carried across a loop and the
+ * compiler never has to copy (and therefore wait on) an in-flight
+ * register. */
+template <int NT, int NB>
+__device__ __forceinline__ void load_blocks(const uint8_t* const (&wp)[NT], int b_first,
+                                            int b_clamp, u4 (&w)[NB][NT]) {
+#pragma unroll
+    for (int p = 0; p < NB; p++) {
+        const int bb = min(b_first + p, b_clamp);
+#pragma unroll
+        for (int s = 0; s < NT; s++) w[p][s] = *(const u4*)(wp[s] + (size_t)bb * 64);
+    }
+}
+
+/* Computes the preloaded blocks b_first .. b_first + NB - 1 into tot; the
+ * ones at or past b_end are padding (zero scale). Activations and scales
+ * come from the LDS image, whose K range starts at block xb0 and whose
+ * groups start at g_lo. */
+template <int M, int NG, int NT, int NB, bool HZ>
+__device__ __forceinline__ void compute_blocks(const u4 (&w)[NB][NT], const uint8_t* smem,
+                                               const LdsMap& L, int b_first, int b_end, int xb0,
+                                               int g_lo, int gshift, int col, int j,
+                                               uint32_t m_lo, uint32_t m_hi, uint32_t one024,
+                                               float (&tot)[NT][M]) {
     /* A VALU op reads at most one scalar operand on this target: with the
      * masks in SGPRs every bitfield insert of the unpack splits into an and
      * plus an or. Pinning them to VGPRs (an empty asm emits no instruction)
@@ -284,33 +390,44 @@ __device__ __forceinline__ void stream_blocks(const uint8_t* const (&wp)[NT], co
     const uint16_t* scs = (const uint16_t*)(smem + L.sc_off) + col * L.GS;
     const uint16_t* zcs = (const uint16_t*)(smem + L.zc_off) + col * L.GS;
     const int gamma = (j * NG) / 4;
-    for (int base = b0; base < b1; base += B) {
-        u4 w[B][NT];
 #pragma unroll
-        for (int p = 0; p < B; p++) {
-            const int bb = min(base + p, b1 - 1);
+    for (int p = 0; p < NB; p++) {
+        const int b = b_first + p;
+        const bool live = b < b_end;
+        const int bc = live ? b : xb0;
+        h8 xa[4];
 #pragma unroll
-            for (int s = 0; s < NT; s++) w[p][s] = *(const u4*)(wp[s] + (size_t)bb * 64);
-        }
+        for (int t = 0; t < 4; t++) xa[t] = *(const h8*)(xs + (bc - xb0) * 128 + 8 * t);
+        float sc[NT][NG], zc[NT][NG];
 #pragma unroll
-        for (int p = 0; p < B; p++) {
-            const int b = base + p;
-            const int bc = min(b, b1 - 1);
-            h8 xa[4];
+        for (int g = 0; g < NG; g++) {
+            const int gi = ((bc * NG + g) >> gshift) - g_lo;
 #pragma unroll
-            for (int t = 0; t < 4; t++) xa[t] = *(const h8*)(xs + (bc - xb0) * 128 + 8 * t);
-            float sc[NT][NG], zc[NT][NG];
-#pragma unroll
-            for (int g = 0; g < NG; g++) {
-                const int gi = ((bc * NG + g) >> gshift) - g_lo;
-#pragma unroll
-                for (int s = 0; s < NT; s++) {
-                    sc[s][g] = half_bits_to_float(scs[s * 16 * L.GS + gi]);
-                    zc[s][g] = HZ ? half_bits_to_float(zcs[s * 16 * L.GS + gi]) : 0.0f;
-                }
+            for (int s = 0; s < NT; s++) {
+                sc[s][g] = half_bits_to_float(scs[s * 16 * L.GS + gi]);
+                zc[s][g] = HZ ? half_bits_to_float(zcs[s * 16 * L.GS + gi]) : 0.0f;
             }
-            block_step<M, NG, NT, HZ>(xa, w[p], gamma, sc, zc, b < b1, m_lo, m_hi, one024, tot);
         }
+        block_step<M, NG, NT, HZ>(xa, w[p], gamma, sc, zc, live, m_lo, m_hi, one024, tot);
+    }
+}
+
+/* Copies M activation rows [M][K] (fp16) into the LDS x image, permuting
+ * each 8-element block into unpack8_magic slot order with odd elements
+ * divided by 16 (exact: a power-of-two scale). 16-byte accesses. */
+template <int M>
+__device__ __forceinline__ void stage_x_perm(uint8_t* smem, const LdsMap& L,
+                                             const uint16_t* __restrict__ src, int K) {
+    uint16_t* xs = (uint16_t*)(smem + L.x_off);
+    const int per_row = K / 8;
+    const f16 sixteenth = (f16)0.0625f;
+    for (int i = threadIdx.x; i < M * per_row; i += blockDim.x) {
+        const int v = i / per_row, c = i - v * per_row;
+        const h8 in = __builtin_bit_cast(h8, *(const u4*)(src + (size_t)v * K + c * 8));
+        h8 o;
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[perm_slot(e)] = (e & 1) ? in[e] * sixteenth : in[e];
+        *(h8*)(xs + v * L.XR + c * 8) = o;
     }
 }
 
@@ -320,7 +437,7 @@ __device__ __forceinline__ void stream_blocks(const uint8_t* const (&wp)[NT], co
 
 /* grid (inter / (16 TILES), max_u); workgroup = TILES gate + TILES up row
  * tiles of unique expert blockIdx.y over the full hidden K, waves split K. */
-template <int M, int NG, int TILES, int PF, bool HZ>
+template <int M, int NG, int TILES, int NB, bool HZ>
 __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void gateup_kernel(const DecodeParams P) {
     constexpr int NT = 2 * TILES;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -333,7 +450,8 @@ __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void gateup_kernel(const Decode
     const int r0 = blockIdx.x * 16 * TILES;
     const int nblk = K >> 7;
     const int G = K / P.gs;
-    const int b0 = wave * nblk / nw, b1 = (wave + 1) * nblk / nw;
+    /* wave w owns blocks [NB w, NB w + NB); the host launches ceil(nblk/NB) waves */
+    const int b0 = wave * NB, b1 = min(b0 + NB, nblk);
     const LdsMap L = lds_map(M, NT, K, G, HZ, nw);
 
     const uint8_t* wp[NT];
@@ -342,16 +460,46 @@ __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void gateup_kernel(const Decode
         const int mat = s < TILES ? 0 : 1;
         wp[s] = blob + P.p_off[mat] + (size_t)(r0 + 16 * (s % TILES) + col) * (K / 2) + 16 * j;
     }
-    stage_x<M>(smem, L, P.xperm, K, 0, K);
+    /* Order of issue: activations and the tile's scales (small, read by
+     * the whole workgroup), then all of this wave's weights; the LDS writes
+     * then wait only for the former. The scales (and zeros) of 16
+     * consecutive rows are one contiguous run of 32 G bytes. */
+    constexpr int XCNT = M * NB / 4 > 0 ? M * NB / 4 : 1;
+    constexpr int SCNT = NB * NG / 16 > 0 ? NB * NG / 16 : 1;
+    Stage16<XCNT> sx;
+    Stage16<SCNT> ssc[NT], szc[NT];
+    const bool fast = Stage16<XCNT>::ok(M, K / 8) && Stage16<SCNT>::ok(1, 2 * G);
+    if (fast) {
+        sx.issue((const uint8_t*)P.xh, (size_t)K * 2, M, K / 8);
 #pragma unroll
-    for (int s = 0; s < NT; s++) {
-        const int mat = s < TILES ? 0 : 1;
-        const int rt = r0 + 16 * (s % TILES);
-        stage_groups((uint16_t*)(smem + L.sc_off) + s * 16 * G,
-                     (const uint16_t*)(blob + P.s_off[mat]), G, rt, 0, G);
-        if (HZ)
-            stage_groups((uint16_t*)(smem + L.zc_off) + s * 16 * G,
-                         (const uint16_t*)(blob + P.z_off[mat]), G, rt, 0, G);
+        for (int s = 0; s < NT; s++) {
+            const int mat = s < TILES ? 0 : 1;
+            const size_t roff = (size_t)(r0 + 16 * (s % TILES)) * G * 2;
+            ssc[s].issue(blob + P.s_off[mat] + roff, 0, 1, 2 * G);
+            if (HZ) szc[s].issue(blob + P.z_off[mat] + roff, 0, 1, 2 * G);
+        }
+    }
+    u4 w[NB][NT];
+    load_blocks<NT, NB>(wp, b0, nblk - 1, w);
+    if (fast) {
+        sx.template commit<true>(smem + L.x_off, L.XR * 2);
+#pragma unroll
+        for (int s = 0; s < NT; s++) {
+            ssc[s].template commit<false>(smem + L.sc_off + s * 32 * G, 0);
+            if (HZ) szc[s].template commit<false>(smem + L.zc_off + s * 32 * G, 0);
+        }
+    } else {
+        stage_x_perm<M>(smem, L, P.xh, K);
+#pragma unroll
+        for (int s = 0; s < NT; s++) {
+            const int mat = s < TILES ? 0 : 1;
+            const int rt = r0 + 16 * (s % TILES);
+            stage_groups((uint16_t*)(smem + L.sc_off) + s * 16 * G,
+                         (const uint16_t*)(blob + P.s_off[mat]), G, rt, 0, G);
+            if (HZ)
+                stage_groups((uint16_t*)(smem + L.zc_off) + s * 16 * G,
+                             (const uint16_t*)(blob + P.z_off[mat]), G, rt, 0, G);
+        }
     }
     __syncthreads();
 
@@ -360,8 +508,8 @@ __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void gateup_kernel(const Decode
     for (int s = 0; s < NT; s++)
 #pragma unroll
         for (int v = 0; v < M; v++) tot[s][v] = 0.0f;
-    stream_blocks<M, NG, NT, PF, HZ>(wp, smem, L, b0, b1, 0, 0, P.gshift, col, j, P.m_lo, P.m_hi,
-                                     P.one024, tot);
+    compute_blocks<M, NG, NT, NB, HZ>(w, smem, L, b0, b1, 0, 0, P.gshift, col, j, P.m_lo, P.m_hi,
+                                      P.one024, tot);
 
     float* red = (float*)(smem + L.red_off);
     if (lane < 16) {
@@ -395,38 +543,74 @@ __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void gateup_kernel(const Decode
  * unique expert u, K chunk c of DEC_CHUNK_BLOCKS blocks) writes
  * part[u][c][v][row] = down_u[row, chunk] . h'_u[v][chunk] (routing weight
  * already folded into h'). */
-template <int M, int NG, int TILES, int PF, bool HZ>
+template <int M, int NG, int TILES, int NB, bool HZ>
 __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void down_kernel(const DecodeParams P) {
     constexpr int NT = TILES;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int nch = P.n_chunks;
     const int u = blockIdx.y / nch, c = blockIdx.y - u * nch;
+    const int r0 = blockIdx.x * 16 * TILES;
     if (u >= *P.n_unique) return;
     const uint8_t* blob = P.ublob[u];
     const int K = P.inter, H = P.hidden;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int col = lane & 15, j = lane >> 4;
-    const int r0 = blockIdx.x * 16 * TILES;
     const int nblk = K >> 7;
     const int G = K / P.gs;
     const int cb0 = c * DEC_CHUNK_BLOCKS, cb1 = min(cb0 + DEC_CHUNK_BLOCKS, nblk);
     const int g_lo = (cb0 * NG) >> P.gshift, g_hi = (((cb1 * NG) - 1) >> P.gshift) + 1;
     const int nb = cb1 - cb0;
-    const int b0 = cb0 + wave * nb / nw, b1 = cb0 + (wave + 1) * nb / nw;
+    /* wave w owns blocks [cb0 + NB w, cb0 + NB w + NB) of the chunk */
+    const int b0 = cb0 + wave * NB, b1 = min(b0 + NB, cb1);
     const LdsMap L = lds_map(M, NT, DEC_CHUNK_BLOCKS * 128, g_hi - g_lo, HZ, nw);
 
     const uint8_t* wp[NT];
 #pragma unroll
     for (int s = 0; s < NT; s++)
         wp[s] = blob + P.p_off[2] + (size_t)(r0 + 16 * s + col) * (K / 2) + 16 * j;
-    stage_x<M>(smem, L, P.hperm + (size_t)u * M * K, K, cb0 * 128, nb * 128);
+    /* Same order as the gate/up kernel: h' chunk and scales, then weights.
+     * A row's scales of the chunk are (g_hi - g_lo) * 2 bytes at a row
+     * stride of 2 G bytes; 16-byte pieces need both to be multiples of 16
+     * (always true for a single chunk: then the 16 rows are contiguous). */
+    constexpr int XCNT = M * NB / 4 > 0 ? M * NB / 4 : 1;
+    constexpr int SCNT = NB * NG / 16 > 0 ? NB * NG / 16 : 1;
+    const int gn = g_hi - g_lo;
+    const bool one_run = nch == 1;
+    const int s_rows = one_run ? 1 : 16;
+    const int s_w16 = one_run ? 2 * G : gn / 8;
+    const bool fast = Stage16<XCNT>::ok(M, nb * 16) && Stage16<SCNT>::ok(s_rows, s_w16) &&
+                      (one_run || (G % 8 == 0 && g_lo % 8 == 0 && gn % 8 == 0));
+    Stage16<XCNT> sx;
+    Stage16<SCNT> ssc[NT], szc[NT];
+    if (fast) {
+        sx.issue((const uint8_t*)(P.hperm + (size_t)u * M * K + cb0 * 128), (size_t)K * 2, M,
+                 nb * 16);
 #pragma unroll
-    for (int s = 0; s < NT; s++) {
-        stage_groups((uint16_t*)(smem + L.sc_off) + s * 16 * L.GS,
-                     (const uint16_t*)(blob + P.s_off[2]), G, r0 + 16 * s, g_lo, L.GS);
-        if (HZ)
-            stage_groups((uint16_t*)(smem + L.zc_off) + s * 16 * L.GS,
-                         (const uint16_t*)(blob + P.z_off[2]), G, r0 + 16 * s, g_lo, L.GS);
+        for (int s = 0; s < NT; s++) {
+            const size_t roff = ((size_t)(r0 + 16 * s) * G + g_lo) * 2;
+            ssc[s].issue(blob + P.s_off[2] + roff, (size_t)G * 2, s_rows, s_w16);
+            if (HZ) szc[s].issue(blob + P.z_off[2] + roff, (size_t)G * 2, s_rows, s_w16);
+        }
+    }
+    u4 w[NB][NT];
+    load_blocks<NT, NB>(wp, b0, cb1 - 1, w);
+    if (fast) {
+        sx.template commit<false>(smem + L.x_off, L.XR * 2);
+#pragma unroll
+        for (int s = 0; s < NT; s++) {
+            ssc[s].template commit<false>(smem + L.sc_off + s * 32 * L.GS, L.GS * 2);
+            if (HZ) szc[s].template commit<false>(smem + L.zc_off + s * 32 * L.GS, L.GS * 2);
+        }
+    } else {
+        stage_x<M>(smem, L, P.hperm + (size_t)u * M * K, K, cb0 * 128, nb * 128);
+#pragma unroll
+        for (int s = 0; s < NT; s++) {
+            stage_groups((uint16_t*)(smem + L.sc_off) + s * 16 * L.GS,
+                         (const uint16_t*)(blob + P.s_off[2]), G, r0 + 16 * s, g_lo, L.GS);
+            if (HZ)
+                stage_groups((uint16_t*)(smem + L.zc_off) + s * 16 * L.GS,
+                             (const uint16_t*)(blob + P.z_off[2]), G, r0 + 16 * s, g_lo, L.GS);
+        }
     }
     __syncthreads();
 
@@ -435,8 +619,8 @@ __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void down_kernel(const DecodePa
     for (int s = 0; s < NT; s++)
 #pragma unroll
         for (int v = 0; v < M; v++) tot[s][v] = 0.0f;
-    stream_blocks<M, NG, NT, PF, HZ>(wp, smem, L, b0, b1, cb0, g_lo, P.gshift, col, j, P.m_lo,
-                                     P.m_hi, P.one024, tot);
+    compute_blocks<M, NG, NT, NB, HZ>(w, smem, L, b0, b1, cb0, g_lo, P.gshift, col, j, P.m_lo,
+                                      P.m_hi, P.one024, tot);
 
     float* red = (float*)(smem + L.red_off);
     if (lane < 16) {
@@ -455,22 +639,29 @@ __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void down_kernel(const DecodePa
 }
 
 /* out[v][r] (+)= sum over unique experts u (list order) and K chunks c of
- * part[u][c][v][r]. */
-__global__ __launch_bounds__(256) void combine_kernel(const DecodeParams P, int M, float* out32,
-                                                      uint16_t* out16, int accumulate) {
-    const int n_u = *P.n_unique;
-    const int H = P.hidden, nch = P.n_chunks;
+ * part[u][c][v][r]. All loads of a thread are issued before the sum. */
+__global__ __launch_bounds__(256) void combine_kernel(const DecodeParams P) {
+    constexpr int MAXQ = 16;
+    const int n_q = *P.n_unique * P.n_chunks;
+    const int H = P.hidden;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= M * H) return;
+    if (i >= P.M * H) return;
     const int v = i / H, r = i - v * H;
+    const size_t stride = (size_t)P.M * H;
+    const float* src = P.part + (size_t)v * H + r;
     float y = 0.0f;
-    for (int u = 0; u < n_u; u++)
-        for (int c = 0; c < nch; c++) y += P.part[(((size_t)u * nch + c) * M + v) * H + r];
-    if (out32) {
-        if (accumulate) y += out32[i];
-        out32[i] = y;
+    for (int q0 = 0; q0 < n_q; q0 += MAXQ) {
+        float t[MAXQ];
+#pragma unroll
+        for (int q = 0; q < MAXQ; q++) t[q] = (q0 + q < n_q) ? src[(size_t)(q0 + q) * stride] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < MAXQ; q++) y += t[q];
     }
-    if (out16) out16[i] = __builtin_bit_cast(uint16_t, (f16)y);
+    if (P.out32) {
+        if (P.accumulate) y += P.out32[i];
+        P.out32[i] = y;
+    }
+    if (P.out16) P.out16[i] = __builtin_bit_cast(uint16_t, (f16)y);
 }
 
 /* ======================================================================= */
@@ -484,6 +675,7 @@ extern "C" hipError_t wisp_expert_layout_check(const WispExpertLayout* L) {
         L->cols[2] != inter)
         return hipErrorInvalidValue;
     if (inter == 0 || hidden == 0 || inter % 128 || hidden % 128) return hipErrorInvalidValue;
+    if (hidden / 128 > 16 * DEC_MAX_WAVES) return hipErrorInvalidValue;   /* gate/up waves */
     const uint64_t gs = L->group_size;
     const bool gs_ok = gs >= 32 && (gs & (gs - 1)) == 0;
     if (!gs_ok || hidden % gs || inter % gs) return hipErrorInvalidValue;
@@ -499,7 +691,7 @@ extern "C" hipError_t wisp_expert_layout_check(const WispExpertLayout* L) {
 }
 
 struct WsLayout {
-    size_t nu, ublob, uw, xperm, hperm, part, total;
+    size_t nu, ublob, uw, xconv, hperm, part, total;
     int max_u;
 };
 
@@ -510,7 +702,7 @@ static WsLayout ws_layout(const WispExpertLayout* L, int M, int top_k, int has_s
     w.nu = off; off += 256;
     w.ublob = off; off = align_up(off + (size_t)w.max_u * sizeof(void*), 256);
     w.uw = off; off = align_up(off + (size_t)w.max_u * 4 * sizeof(float), 256);
-    w.xperm = off; off = align_up(off + (size_t)M * L->cols[0] * 2, 256);
+    w.xconv = off; off = align_up(off + (size_t)M * L->cols[0] * 2, 256);
     w.hperm = off; off = align_up(off + (size_t)w.max_u * M * L->rows[0] * 2, 256);
     const size_t nch = ((L->rows[0] / 128) + DEC_CHUNK_BLOCKS - 1) / DEC_CHUNK_BLOCKS;
     w.part = off; off = align_up(off + (size_t)w.max_u * nch * M * L->cols[0] * 4, 256);
@@ -525,41 +717,28 @@ extern "C" size_t wisp_moe_decode_workspace_bytes(const WispExpertLayout* L, int
     return ws_layout(L, n_tokens, top_k, has_shared).total;
 }
 
-/* Launch shape of the two expert kernels. Values <= 0 select the built-in
- * heuristic. Set only through wisp_amd__decode_config (tuning sweeps). */
-struct DecodeCfg {
-    int gu_tiles, gu_waves, gu_pf, dn_tiles, dn_waves, dn_pf;
-};
-static DecodeCfg g_dec_cfg = {0, 0, 0, 0, 0, 0};
+/* Blocks of 128 weights per wave: each wave issues all its weight loads at
+ * once (NB x 16 B per row tile and lane). */
+static int blocks_per_wave(int nblk) { return nblk > 8 * DEC_MAX_WAVES ? 16 : 8; }
 
-extern "C" void wisp_amd__decode_config(int gu_tiles, int gu_waves, int gu_pf, int dn_tiles,
-                                        int dn_waves, int dn_pf) {
-    g_dec_cfg = {gu_tiles, gu_waves, gu_pf, dn_tiles, dn_waves, dn_pf};
-}
-
-/* Waves per workgroup so that each wave streams about `per_wave` blocks. */
-static int waves_for(int blocks_total, int per_wave, int max_waves) {
-    int w = blocks_total / per_wave;
-    if (w < 1) w = 1;
-    if (w > max_waves) w = max_waves;
-    return w;
-}
-
-template <int M, int NG, int TILES, int PF, bool HZ>
-static void launch_gateup(const DecodeParams& P, int waves, hipStream_t s) {
+template <int M, int NG, int TILES, int NB, bool HZ>
+static void launch_gateup(const DecodeParams& P, hipStream_t s) {
+    const int waves = (P.hidden / 128 + NB - 1) / NB;
     const LdsMap L = lds_map(M, 2 * TILES, P.hidden, P.hidden / P.gs, HZ, waves);
-    auto k = gateup_kernel<M, NG, TILES, PF, HZ>;
+    auto k = gateup_kernel<M, NG, TILES, NB, HZ>;
     if (L.bytes > 65536)
         (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, L.bytes);
     hipLaunchKernelGGL(k, dim3(P.inter / (16 * TILES), P.max_u), dim3(64 * waves), L.bytes, s, P);
 }
 
-template <int M, int NG, int TILES, int PF, bool HZ>
-static void launch_down(const DecodeParams& P, int waves, hipStream_t s) {
+template <int M, int NG, int TILES, int NB, bool HZ>
+static void launch_down(const DecodeParams& P, hipStream_t s) {
+    const int chunk = (P.inter / 128) < DEC_CHUNK_BLOCKS ? (P.inter / 128) : DEC_CHUNK_BLOCKS;
+    const int waves = (chunk + NB - 1) / NB;
     /* LDS sized for the largest chunk: full DEC_CHUNK_BLOCKS and its groups */
     const int ng_hi = (((DEC_CHUNK_BLOCKS * NG) - 1) >> P.gshift) + 2;
     const LdsMap L = lds_map(M, TILES, DEC_CHUNK_BLOCKS * 128, ng_hi, HZ, waves);
-    auto k = down_kernel<M, NG, TILES, PF, HZ>;
+    auto k = down_kernel<M, NG, TILES, NB, HZ>;
     if (L.bytes > 65536)
         (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, L.bytes);
     hipLaunchKernelGGL(k, dim3(P.hidden / (16 * TILES), P.max_u * P.n_chunks), dim3(64 * waves),
@@ -567,77 +746,42 @@ static void launch_down(const DecodeParams& P, int waves, hipStream_t s) {
 }
 
 template <int M, int NG, bool HZ>
-static void launch_compute(const DecodeParams& P, float* out32, uint16_t* out16, int accumulate,
-                           hipStream_t s) {
-    const DecodeCfg c = g_dec_cfg;
-    const int gu_waves = c.gu_waves > 0 ? (c.gu_waves > DEC_MAX_WAVES ? DEC_MAX_WAVES : c.gu_waves)
-                                        : waves_for(P.hidden / 128, 8, 4);
-    const int chunk = (P.inter / 128) < DEC_CHUNK_BLOCKS ? (P.inter / 128) : DEC_CHUNK_BLOCKS;
-    const int dn_waves = c.dn_waves > 0 ? (c.dn_waves > DEC_MAX_WAVES ? DEC_MAX_WAVES : c.dn_waves)
-                                        : waves_for(chunk, 8, 4);
-    /* Defaults (measured on MI355X at the Mixtral and DeepSeek-V3 decode
-     * shapes): one row tile per matrix, batches of 2 blocks, about 8 blocks
-     * per wave and at most 4 waves. Other tile / batch variants are built
-     * for the common case only (group size >= 128, no zero points). */
-    auto variant = [](int tiles, int pf) { return 10 * (tiles == 2 ? 2 : 1) + (pf == 8 ? 8 : (pf == 4 ? 4 : 2)); };
-    const int gv = (NG == 1 && !HZ) ? variant(c.gu_tiles, c.gu_pf) : 0;
-    const int dv = (NG == 1 && !HZ) ? variant(c.dn_tiles, c.dn_pf) : 0;
+static void launch_compute(const DecodeParams& P, hipStream_t s) {
     ev_before(EV_GATEUP, s);
-    switch (gv) {
-        case 12: launch_gateup<M, 1, 1, 2, false>(P, gu_waves, s); break;
-        case 14: launch_gateup<M, 1, 1, 4, false>(P, gu_waves, s); break;
-        case 18: launch_gateup<M, 1, 1, 8, false>(P, gu_waves, s); break;
-        case 22: launch_gateup<M, 1, 2, 2, false>(P, gu_waves, s); break;
-        case 24: launch_gateup<M, 1, 2, 4, false>(P, gu_waves, s); break;
-        default: launch_gateup<M, NG, 1, 2, HZ>(P, gu_waves, s); break;
-    }
+    if (blocks_per_wave(P.hidden / 128) == 16) launch_gateup<M, NG, 1, 16, HZ>(P, s);
+    else launch_gateup<M, NG, 1, 8, HZ>(P, s);
     ev_after(EV_GATEUP, s);
     ev_before(EV_DOWN, s);
-    switch (dv) {
-        case 12: launch_down<M, 1, 1, 2, false>(P, dn_waves, s); break;
-        case 14: launch_down<M, 1, 1, 4, false>(P, dn_waves, s); break;
-        case 18: launch_down<M, 1, 1, 8, false>(P, dn_waves, s); break;
-        case 22: launch_down<M, 1, 2, 2, false>(P, dn_waves, s); break;
-        case 24: launch_down<M, 1, 2, 4, false>(P, dn_waves, s); break;
-        default: launch_down<M, NG, 1, 2, HZ>(P, dn_waves, s); break;
-    }
+    launch_down<M, NG, 1, 8, HZ>(P, s);
     ev_after(EV_DOWN, s);
     ev_before(EV_COMBINE, s);
-    const int n = M * P.hidden;
-    hipLaunchKernelGGL(combine_kernel, dim3((n + 255) / 256), dim3(256), 0, s, P, M, out32, out16,
-                       accumulate);
+    hipLaunchKernelGGL(combine_kernel, dim3((M * P.hidden + 255) / 256), dim3(256), 0, s, P);
     ev_after(EV_COMBINE, s);
 }
 
 template <int M>
-static void launch_ng(int ng, bool hz, const DecodeParams& P, float* o32, uint16_t* o16, int acc,
-                      hipStream_t s) {
+static void launch_ng(int ng, bool hz, const DecodeParams& P, hipStream_t s) {
     if (ng == 1) {
-        if (hz) launch_compute<M, 1, true>(P, o32, o16, acc, s);
-        else launch_compute<M, 1, false>(P, o32, o16, acc, s);
+        if (hz) launch_compute<M, 1, true>(P, s);
+        else launch_compute<M, 1, false>(P, s);
     } else if (ng == 2) {
-        if (hz) launch_compute<M, 2, true>(P, o32, o16, acc, s);
-        else launch_compute<M, 2, false>(P, o32, o16, acc, s);
+        if (hz) launch_compute<M, 2, true>(P, s);
+        else launch_compute<M, 2, false>(P, s);
     } else {
-        if (hz) launch_compute<M, 4, true>(P, o32, o16, acc, s);
-        else launch_compute<M, 4, false>(P, o32, o16, acc, s);
+        if (hz) launch_compute<M, 4, true>(P, s);
+        else launch_compute<M, 4, false>(P, s);
     }
 }
 
-extern "C" hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table,
-                                               const void* d_shared_blob,
-                                               const WispExpertLayout* L, const void* d_x,
-                                               int x_dtype, int n_tokens, const int* d_topk_idx,
-                                               const float* d_topk_w, int top_k, int n_experts,
-                                               void* d_workspace, size_t workspace_bytes,
-                                               int accumulate, float* d_out_f32,
-                                               wisp_half* d_out_f16, hipStream_t s) {
-    if (n_tokens < 1 || n_tokens > DEC_MAX_TOKENS || top_k < 1 || top_k > DEC_MAX_TOPK ||
-        n_experts < 1 || !d_expert_table || !d_x || !d_topk_idx || !d_topk_w || !d_workspace ||
-        (!d_out_f32 && !d_out_f16) || (x_dtype != WISP_DTYPE_F16 && x_dtype != WISP_DTYPE_F32))
-        return hipErrorInvalidValue;
+/* Shared body of the two decode entry points: R.mode selects where the
+ * routing comes from (see RouteArgs). */
+static hipError_t decode_run(const void* const* d_expert_table, const void* d_shared_blob,
+                             const WispExpertLayout* L, const void* d_x, int x_dtype, int M,
+                             RouteArgs R, int top_k, int n_experts, void* d_workspace,
+                             size_t workspace_bytes, int accumulate, float* d_out_f32,
+                             wisp_half* d_out_f16, hipStream_t s) {
     if (wisp_expert_layout_check(L) != hipSuccess) return hipErrorInvalidValue;
-    const WsLayout w = ws_layout(L, n_tokens, top_k, d_shared_blob != nullptr);
+    const WsLayout w = ws_layout(L, M, top_k, d_shared_blob != nullptr);
     if (workspace_bytes < w.total) return hipErrorInvalidValue;
 
     DecodeParams P;
@@ -661,36 +805,105 @@ extern "C" hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table
     P.m_hi = 0x00F000F0u;
     P.one024 = 0x64006400u;
     P.max_u = w.max_u;
+    P.M = M;
     char* ws = (char*)d_workspace;
     P.n_unique = (int*)(ws + w.nu);
     P.ublob = (const uint8_t**)(ws + w.ublob);
     P.uw = (float*)(ws + w.uw);
-    P.xperm = (uint16_t*)(ws + w.xperm);
+    const bool x_direct = x_dtype == WISP_DTYPE_F16 && ((uintptr_t)d_x % 16) == 0;
+    P.xconv = x_direct ? nullptr : (uint16_t*)(ws + w.xconv);
+    P.xh = x_direct ? (const uint16_t*)d_x : P.xconv;
     P.hperm = (uint16_t*)(ws + w.hperm);
     P.part = (float*)(ws + w.part);
+    P.out32 = d_out_f32;
+    P.out16 = (uint16_t*)d_out_f16;
+    P.accumulate = accumulate ? 1 : 0;
 
-    const int prep_blocks = 1 + (n_tokens * (P.hidden / 8) + 255) / 256;
+    const size_t xsz = x_dtype == WISP_DTYPE_F16 ? 2 : 4;
+    const size_t lds = R.mode == 0 ? 0
+                       : align_up_dev(2 * M * n_experts * 4, 16) +
+                             (R.mode == 2 ? M * P.hidden * xsz : 0);
     ev_before(EV_PREP, s);
     if (x_dtype == WISP_DTYPE_F16)
-        hipLaunchKernelGGL(decode_prep_kernel<uint16_t>, dim3(prep_blocks), dim3(256), 0, s, P,
-                           d_expert_table, d_shared_blob, (const uint16_t*)d_x, n_tokens,
-                           d_topk_idx, d_topk_w, top_k, n_experts);
+        hipLaunchKernelGGL(decode_prep_kernel<uint16_t>, dim3(1), dim3(DEC_PREP_THREADS), lds, s, P, R,
+                           d_expert_table, d_shared_blob, (const uint16_t*)d_x, top_k, n_experts);
     else
-        hipLaunchKernelGGL(decode_prep_kernel<float>, dim3(prep_blocks), dim3(256), 0, s, P,
-                           d_expert_table, d_shared_blob, (const float*)d_x, n_tokens,
-                           d_topk_idx, d_topk_w, top_k, n_experts);
+        hipLaunchKernelGGL(decode_prep_kernel<float>, dim3(1), dim3(DEC_PREP_THREADS), lds, s, P, R,
+                           d_expert_table, d_shared_blob, (const float*)d_x, top_k, n_experts);
     ev_after(EV_PREP, s);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
 
-    const int gs = P.gs;
-    const int ng = gs >= 128 ? 1 : 128 / gs;
+    const int ng = P.gs >= 128 ? 1 : 128 / P.gs;
     const bool hz = P.has_zeros != 0;
-    switch (n_tokens) {
-        case 1: launch_ng<1>(ng, hz, P, d_out_f32, d_out_f16, accumulate, s); break;
-        case 2: launch_ng<2>(ng, hz, P, d_out_f32, d_out_f16, accumulate, s); break;
-        case 3: launch_ng<3>(ng, hz, P, d_out_f32, d_out_f16, accumulate, s); break;
-        default: launch_ng<4>(ng, hz, P, d_out_f32, d_out_f16, accumulate, s); break;
+    switch (M) {
+        case 1: launch_ng<1>(ng, hz, P, s); break;
+        case 2: launch_ng<2>(ng, hz, P, s); break;
+        case 3: launch_ng<3>(ng, hz, P, s); break;
+        default: launch_ng<4>(ng, hz, P, s); break;
     }
     return hipGetLastError();
+}
+
+static bool decode_args_ok(const void* table, const void* x, int x_dtype, int M, int top_k,
+                           int n_experts, const void* ws, const float* o32, const wisp_half* o16) {
+    return M >= 1 && M <= DEC_MAX_TOKENS && top_k >= 1 && top_k <= DEC_MAX_TOPK &&
+           n_experts >= 1 && table && x && ws && (o32 || o16) &&
+           (x_dtype == WISP_DTYPE_F16 || x_dtype == WISP_DTYPE_F32);
+}
+
+extern "C" hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table,
+                                               const void* d_shared_blob,
+                                               const WispExpertLayout* L, const void* d_x,
+                                               int x_dtype, int n_tokens, const int* d_topk_idx,
+                                               const float* d_topk_w, int top_k, int n_experts,
+                                               void* d_workspace, size_t workspace_bytes,
+                                               int accumulate, float* d_out_f32,
+                                               wisp_half* d_out_f16, hipStream_t s) {
+    if (!decode_args_ok(d_expert_table, d_x, x_dtype, n_tokens, top_k, n_experts, d_workspace,
+                        d_out_f32, d_out_f16) || !d_topk_idx || !d_topk_w)
+        return hipErrorInvalidValue;
+    RouteArgs R = {nullptr, nullptr, 0, 0, nullptr, (int*)d_topk_idx, (float*)d_topk_w};
+    return decode_run(d_expert_table, d_shared_blob, L, d_x, x_dtype, n_tokens, R, top_k,
+                      n_experts, d_workspace, workspace_bytes, accumulate, d_out_f32, d_out_f16, s);
+}
+
+/* Raw router logits for the prep kernel when the router matrix is too large
+ * to run inside it (defined in moe_route.hip). */
+hipError_t wisp_amd__router_logits(const wisp_half* W, const wisp_half* bias, const void* x,
+                                   int x_dtype, int n_tokens, int hidden, int n_experts,
+                                   int add_bias, float* logits, hipStream_t s);
+
+extern "C" hipError_t wisp_gpu_moe_layer_decode_int4(
+    const wisp_half* d_router_w, const wisp_half* d_router_bias, int router_kind,
+    float* d_scores, int* d_topk_idx, float* d_topk_w, const void* const* d_expert_table,
+    const void* d_shared_blob, const WispExpertLayout* L, const void* d_x, int x_dtype,
+    int n_tokens, int top_k, int n_experts, void* d_workspace, size_t workspace_bytes,
+    int accumulate, float* d_out_f32, wisp_half* d_out_f16, hipStream_t s) {
+    if (!decode_args_ok(d_expert_table, d_x, x_dtype, n_tokens, top_k, n_experts, d_workspace,
+                        d_out_f32, d_out_f16) ||
+        !d_router_w || !d_scores || !d_topk_idx || !d_topk_w || top_k > n_experts ||
+        n_experts > DEC_ROUTE_MAX_EXPERTS ||
+        (router_kind != WISP_ROUTER_SOFTMAX && router_kind != WISP_ROUTER_SIGMOID))
+        return hipErrorInvalidValue;
+    if (wisp_expert_layout_check(L) != hipSuccess) return hipErrorInvalidValue;
+    const int hidden = (int)L->cols[0];
+    const size_t xsz = x_dtype == WISP_DTYPE_F16 ? 2 : 4;
+    const size_t prep_lds = align_up_dev(2 * n_tokens * n_experts * 4, 16) + n_tokens * hidden * xsz;
+    const bool fuse = (size_t)n_experts * hidden * 2 <= DEC_ROUTE_FUSE_BYTES &&
+                      hidden <= ROUTE_UNROLL * WAVE * 8 &&
+                      prep_lds <= 65536 && (uintptr_t)d_router_w % 16 == 0 &&
+                      (uintptr_t)d_x % 16 == 0;
+    RouteArgs R = {(const uint16_t*)d_router_w, (const uint16_t*)d_router_bias, router_kind,
+                   fuse ? 2 : 1, d_scores, d_topk_idx, d_topk_w};
+    if (!fuse) {
+        ev_before(EV_ROUTE, s);
+        hipError_t e = wisp_amd__router_logits(d_router_w, d_router_bias, d_x, x_dtype, n_tokens,
+                                               hidden, n_experts,
+                                               router_kind == WISP_ROUTER_SOFTMAX, d_scores, s);
+        ev_after(EV_ROUTE, s);
+        if (e != hipSuccess) return e;
+    }
+    return decode_run(d_expert_table, d_shared_blob, L, d_x, x_dtype, n_tokens, R, top_k,
+                      n_experts, d_workspace, workspace_bytes, accumulate, d_out_f32, d_out_f16, s);
 }

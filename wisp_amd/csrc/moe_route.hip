@@ -12,24 +12,16 @@
  */
 #include <mutex>
 
-#include "hip_common.h"
-
-#define ROUTE_MAX_TOPK 64
-#define ROUTE_MAX_EXPERTS 1024
-#define ROUTE_TOK_PER_WG 4
+#include "route_common.h"
 
 /* ======================================================================= */
 /* router logits: one wave per expert row, up to 4 tokens per pass           */
 /* ======================================================================= */
 
-template <typename XT>
-__device__ __forceinline__ float xval(const XT* x, size_t i);
-template <> __device__ __forceinline__ float xval<float>(const float* x, size_t i) { return x[i]; }
-template <> __device__ __forceinline__ float xval<uint16_t>(const uint16_t* x, size_t i) {
-    return half_bits_to_float(x[i]);
-}
-
-/* logits[t, e] = sum_c W[e, c] x[t, c] (+ bias[e] when add_bias). */
+/* logits[t, e] = sum_c W[e, c] x[t, c] (+ bias[e] when add_bias). The
+ * workgroup's token rows are staged in LDS first (dynamic LDS of
+ * ROUTE_TOK_PER_WG * hidden * sizeof(XT) bytes); W rows need 16-byte
+ * alignment, which the launchers check. */
 template <typename XT>
 __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ W,
                                                             const uint16_t* __restrict__ bias,
@@ -37,6 +29,48 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
                                                             float* __restrict__ logits,
                                                             int n_tokens, int hidden,
                                                             int n_experts, int add_bias) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_raw[];
+    XT* xs = (XT*)lds_raw;
+    const int t0 = blockIdx.y * ROUTE_TOK_PER_WG;
+    const int nt = min(ROUTE_TOK_PER_WG, n_tokens - t0);
+    stage_rows<XT>(xs, x + (size_t)t0 * hidden, nt, hidden);
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    for (int e = blockIdx.x * 4 + (threadIdx.x >> 6); e < n_experts; e += gridDim.x * 4) {
+        float acc[ROUTE_TOK_PER_WG];
+        router_row_dot<XT>(W + (size_t)e * hidden, xs, nt, hidden, lane, acc);
+        const float b = (add_bias && bias) ? half_bits_to_float(bias[e]) : 0.0f;
+#pragma unroll
+        for (int t = 0; t < ROUTE_TOK_PER_WG; t++)
+            if (lane == 0 && t < nt) logits[(size_t)(t0 + t) * n_experts + e] = acc[t] + b;
+    }
+}
+
+/* Launch of router_logits_kernel; false when its requirements (16-byte
+ * aligned W and x, hidden % 8 == 0, token rows fitting 64 KiB of LDS) are
+ * not met. */
+template <typename XT>
+static bool launch_router_logits(const uint16_t* W, const uint16_t* bias, const XT* x,
+                                 float* logits, int n_tokens, int hidden, int n_experts,
+                                 int add_bias, hipStream_t s) {
+    const size_t lds = (size_t)ROUTE_TOK_PER_WG * hidden * sizeof(XT);
+    if (hidden % 8 || (uintptr_t)W % 16 || (uintptr_t)x % 16 || lds > 65536) return false;
+    dim3 grid((n_experts + 3) / 4, (n_tokens + ROUTE_TOK_PER_WG - 1) / ROUTE_TOK_PER_WG);
+    hipLaunchKernelGGL(router_logits_kernel<XT>, grid, dim3(256), lds, s, W, bias, x, logits,
+                       n_tokens, hidden, n_experts, add_bias);
+    return true;
+}
+
+/* Any alignment and hidden size: one wave per expert row, scalar loads
+ * (the reference kernel's shape, csrc/cuda/router.cu:29-60). Only used when
+ * router_logits_kernel's requirements are not met. */
+template <typename XT>
+__global__ __launch_bounds__(256) void router_logits_any_kernel(const uint16_t* __restrict__ W,
+                                                                const uint16_t* __restrict__ bias,
+                                                                const XT* __restrict__ x,
+                                                                float* __restrict__ logits,
+                                                                int n_tokens, int hidden,
+                                                                int n_experts, int add_bias) {
     const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int t0 = blockIdx.y * ROUTE_TOK_PER_WG;
@@ -44,133 +78,68 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
     const int nt = min(ROUTE_TOK_PER_WG, n_tokens - t0);
     const uint16_t* row = W + (size_t)e * hidden;
     float acc[ROUTE_TOK_PER_WG] = {0.f, 0.f, 0.f, 0.f};
-    const bool vec = (hidden % 8 == 0) && ((uintptr_t)row % 16 == 0);
-    if (vec) {
-        for (int c8 = lane; c8 < hidden / 8; c8 += WAVE) {
-            h8 w = __builtin_bit_cast(h8, ((const u4*)row)[c8]);
-#pragma unroll
-            for (int t = 0; t < ROUTE_TOK_PER_WG; t++) {
-                if (t < nt) {
-                    const XT* xr = x + (size_t)(t0 + t) * hidden + (size_t)c8 * 8;
-#pragma unroll
-                    for (int i = 0; i < 8; i++)
-                        acc[t] = __builtin_fmaf((float)w[i], xval<XT>(xr, i), acc[t]);
-                }
-            }
-        }
-    } else {
-        for (int c = lane; c < hidden; c += WAVE) {
-            float w = half_bits_to_float(row[c]);
-            for (int t = 0; t < nt; t++)
-                acc[t] = __builtin_fmaf(w, xval<XT>(x, (size_t)(t0 + t) * hidden + c), acc[t]);
-        }
+    for (int c = lane; c < hidden; c += WAVE) {
+        const float w = half_bits_to_float(row[c]);
+        for (int t = 0; t < nt; t++)
+            acc[t] = __builtin_fmaf(w, xval<XT>(x, (size_t)(t0 + t) * hidden + c), acc[t]);
     }
-    float b = (add_bias && bias) ? half_bits_to_float(bias[e]) : 0.0f;
+    const float b = (add_bias && bias) ? half_bits_to_float(bias[e]) : 0.0f;
 #pragma unroll
     for (int t = 0; t < ROUTE_TOK_PER_WG; t++) {
-        float v = wave_sum(acc[t]);
+        const float v = wave_sum(acc[t]);
         if (lane == 0 && t < nt) logits[(size_t)(t0 + t) * n_experts + e] = v + b;
     }
+}
+
+template <typename XT>
+static void router_logits(const uint16_t* W, const uint16_t* bias, const XT* x, float* logits,
+                          int n_tokens, int hidden, int n_experts, int add_bias, hipStream_t s) {
+    if (launch_router_logits<XT>(W, bias, x, logits, n_tokens, hidden, n_experts, add_bias, s))
+        return;
+    dim3 grid((n_experts + 3) / 4, (n_tokens + ROUTE_TOK_PER_WG - 1) / ROUTE_TOK_PER_WG);
+    hipLaunchKernelGGL(router_logits_any_kernel<XT>, grid, dim3(256), 0, s, W, bias, x, logits,
+                       n_tokens, hidden, n_experts, add_bias);
+}
+
+/* Raw logits for the fused layer decode when the router matrix is too large
+ * for its single-workgroup prep (internal; declared in moe_decode.hip). */
+hipError_t wisp_amd__router_logits(const wisp_half* W, const wisp_half* bias, const void* x,
+                                   int x_dtype, int n_tokens, int hidden, int n_experts,
+                                   int add_bias, float* logits, hipStream_t s) {
+    if (x_dtype == WISP_DTYPE_F16)
+        router_logits<uint16_t>(W, bias, (const uint16_t*)x, logits, n_tokens, hidden, n_experts,
+                                add_bias, s);
+    else
+        router_logits<float>(W, bias, (const float*)x, logits, n_tokens, hidden, n_experts,
+                             add_bias, s);
+    return hipGetLastError();
 }
 
 /* ======================================================================= */
 /* top-k: one wave per token                                                */
 /* ======================================================================= */
 
-struct KeyIdx { float v; int i; };
-
-/* a beats b: larger key, or equal key and lower index. NaN never wins. */
-__device__ __forceinline__ bool beats(float av, int ai, float bv, int bi) {
-    return av > bv || (av == bv && ai >= 0 && (bi < 0 || ai < bi));
-}
-
 /* scores_out[t, e] = softmax probability or sigmoid score; idx/w [t, k].
- * For SOFTMAX the logits already include the bias. For SIGMOID the bias
- * (if any) is added to the score for selection only. */
+ * One wave per token; dynamic LDS of 2 * n_experts floats. */
 __global__ __launch_bounds__(64) void topk_kernel(const float* logits,
                                                   const uint16_t* __restrict__ bias,
                                                   float* scores_out,
                                                   int n_tokens, int n_experts, int top_k,
                                                   int kind, int* __restrict__ out_idx,
                                                   float* __restrict__ out_w) {
+    extern __shared__ float topk_lds_buf[];
     const int t = blockIdx.x;
-    const int lane = threadIdx.x;
     if (t >= n_tokens) return;
-    const float* lg = logits + (size_t)t * n_experts;
-    constexpr int PER = ROUTE_MAX_EXPERTS / WAVE;   /* keys per lane */
-    float key[PER], lgt[PER];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-        int e = lane + i * WAVE;
-        float l = e < n_experts ? lg[e] : NAN;
-        lgt[i] = l;
-        float k = l;
-        if (kind == WISP_ROUTER_SIGMOID && bias && e < n_experts)
-            k = 1.0f / (1.0f + __expf(-l)) + half_bits_to_float(bias[e]);
-        key[i] = e < n_experts ? k : NAN;
-        if (e < n_experts) mx = fmaxf(mx, l);
-    }
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, WAVE));
-    /* denominators / scores */
-    float denom = 0.0f;
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-        int e = lane + i * WAVE;
-        if (e < n_experts) {
-            float sc = (kind == WISP_ROUTER_SOFTMAX) ? __expf(lgt[i] - mx)
-                                                     : 1.0f / (1.0f + __expf(-lgt[i]));
-            lgt[i] = sc;
-            denom += sc;
-        }
-    }
-    denom = wave_sum(denom);
-    const float inv = 1.0f / (denom > 0.0f ? denom : 1.0f);
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-        int e = lane + i * WAVE;
-        if (e < n_experts) {
-            if (kind == WISP_ROUTER_SOFTMAX) lgt[i] = lgt[i] * inv;
-            scores_out[(size_t)t * n_experts + e] = lgt[i];
-        }
-    }
-    /* k passes of argmax */
-    uint32_t taken = 0;
-    float wsum = 0.0f;
-    for (int k = 0; k < top_k; k++) {
-        float bv = -INFINITY;
-        int bi = -1;
-        float bs = 0.0f;
-#pragma unroll
-        for (int i = 0; i < PER; i++) {
-            int e = lane + i * WAVE;
-            if (!(taken & (1u << i)) && beats(key[i], e, bv, bi)) {
-                bv = key[i]; bi = e; bs = lgt[i];
-            }
-        }
-        for (int off = 32; off > 0; off >>= 1) {
-            float ov = __shfl_xor(bv, off, WAVE);
-            int oi = __shfl_xor(bi, off, WAVE);
-            float os = __shfl_xor(bs, off, WAVE);
-            if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; bs = os; }
-        }
-        if (bi >= 0 && (bi % WAVE) == lane) taken |= 1u << (bi / WAVE);
-        if (lane == 0) {
-            out_idx[(size_t)t * top_k + k] = bi;
-            float w = bi >= 0 ? bs : 0.0f;
-            out_w[(size_t)t * top_k + k] = w;
-            wsum += w;
-        }
-    }
-    if (lane == 0 && wsum > 0.0f) {
-        for (int k = 0; k < top_k; k++) out_w[(size_t)t * top_k + k] /= wsum;
-    }
+    topk_lds(logits + (size_t)t * n_experts, bias, topk_lds_buf, topk_lds_buf + n_experts,
+             scores_out + (size_t)t * n_experts, n_experts, top_k, kind,
+             out_idx + (size_t)t * top_k, out_w + (size_t)t * top_k, threadIdx.x);
 }
 
 static hipError_t launch_topk(const float* d_logits, const uint16_t* d_bias, float* d_scores,
                               int n_tokens, int n_experts, int top_k, int kind,
                               int* d_idx, float* d_w, hipStream_t s) {
-    hipLaunchKernelGGL(topk_kernel, dim3(n_tokens), dim3(64), 0, s, d_logits, d_bias,
+    hipLaunchKernelGGL(topk_kernel, dim3(n_tokens), dim3(64),
+                       (size_t)2 * n_experts * sizeof(float), s, d_logits, d_bias,
                        d_scores, n_tokens, n_experts, top_k, kind, d_idx, d_w);
     return hipGetLastError();
 }
@@ -194,11 +163,9 @@ extern "C" hipError_t wisp_gpu_moe_route(const wisp_half* d_router_w, const wisp
         top_k <= 0 || top_k > ROUTE_MAX_TOPK || top_k > n_experts ||
         (kind != WISP_ROUTER_SOFTMAX && kind != WISP_ROUTER_SIGMOID))
         return hipErrorInvalidValue;
-    dim3 grid((n_experts + 3) / 4, (n_tokens + ROUTE_TOK_PER_WG - 1) / ROUTE_TOK_PER_WG);
     ev_before(EV_ROUTE, s);
-    hipLaunchKernelGGL(router_logits_kernel<uint16_t>, grid, dim3(256), 0, s, d_router_w,
-                       d_bias, d_x, d_logits, n_tokens, hidden, n_experts,
-                       kind == WISP_ROUTER_SOFTMAX ? 1 : 0);
+    router_logits<uint16_t>(d_router_w, d_bias, d_x, d_logits, n_tokens, hidden, n_experts,
+                            kind == WISP_ROUTER_SOFTMAX ? 1 : 0, s);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     /* the scores overwrite the logits in place: each wave reads its token's
@@ -247,8 +214,7 @@ extern "C" void wisp_gpu_router_topk(const wisp_half* W, const wisp_half* bias, 
     if (n_experts > ROUTE_MAX_EXPERTS || top_k > n_experts) return;
     void *didx, *dw;
     if (!route_stage(&didx, &dw)) return;
-    hipLaunchKernelGGL(router_logits_kernel<float>, dim3((n_experts + 3) / 4, 1), dim3(256), 0,
-                       s, W, bias, x, logits_scratch, 1, hidden, n_experts, 1);
+    router_logits<float>(W, bias, x, logits_scratch, 1, hidden, n_experts, 1, s);
     (void)launch_topk(logits_scratch, nullptr, logits_scratch, 1, n_experts, top_k,
                 WISP_ROUTER_SOFTMAX, (int*)didx, (float*)dw, s);
     (void)hipMemcpyAsync(out_idx, didx, (size_t)top_k * sizeof(int), hipMemcpyDeviceToHost, s);

@@ -53,6 +53,12 @@ def runtime():
             "hipSetDevice": [c_int],
             "hipGetLastError": [],
             "hipMemGetInfo": [POINTER(c_size_t), POINTER(c_size_t)],
+            "hipStreamBeginCapture": [c_void_p, c_int],
+            "hipStreamEndCapture": [c_void_p, POINTER(c_void_p)],
+            "hipGraphInstantiate": [POINTER(c_void_p), c_void_p, c_void_p, c_void_p, c_size_t],
+            "hipGraphLaunch": [c_void_p, c_void_p],
+            "hipGraphExecDestroy": [c_void_p],
+            "hipGraphDestroy": [c_void_p],
         }.items():
             f = getattr(h, name)
             f.argtypes = args
@@ -206,5 +212,40 @@ class Event:
         try:
             if self._e is not None and self._e.value:
                 runtime().hipEventDestroy(self._e)
+        except Exception:
+            pass
+
+
+hipStreamCaptureModeThreadLocal = 1
+
+
+class Graph:
+    """A HIP graph captured from the launches `fn()` makes on `stream`,
+    instantiated for replay with launch()."""
+
+    def __init__(self, stream: Stream, fn):
+        rt = runtime()
+        check(rt.hipStreamBeginCapture(c_void_p(stream.handle), hipStreamCaptureModeThreadLocal),
+              "hipStreamBeginCapture")
+        try:
+            fn()
+        finally:
+            g = c_void_p()
+            rc = rt.hipStreamEndCapture(c_void_p(stream.handle), byref(g))
+        check(rc, "hipStreamEndCapture")
+        self._g = g
+        ex = c_void_p()
+        check(rt.hipGraphInstantiate(byref(ex), g, None, None, 0), "hipGraphInstantiate")
+        self._ex = ex
+
+    def launch(self, stream: Stream) -> None:
+        check(runtime().hipGraphLaunch(self._ex, c_void_p(stream.handle)), "hipGraphLaunch")
+
+    def __del__(self):
+        try:
+            if self._ex is not None and self._ex.value:
+                runtime().hipGraphExecDestroy(self._ex)
+            if self._g is not None and self._g.value:
+                runtime().hipGraphDestroy(self._g)
         except Exception:
             pass

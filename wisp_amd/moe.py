@@ -87,6 +87,20 @@ def moe_decode_int4(table: int, shared_blob: int, layout: WispExpertLayout, x: i
     _ck(rc, "wisp_gpu_moe_decode_int4")
 
 
+def moe_layer_decode_int4(router_w: int, router_bias: int, kind: int, scores: int, idx: int,
+                          w: int, table: int, shared_blob: int, layout: WispExpertLayout, x: int,
+                          n_tokens: int, top_k: int, n_experts: int, ws: DeviceBuffer,
+                          out32: int = 0, out16: int = 0, stream: int = 0,
+                          accumulate: bool = False, x_dtype: int = DTYPE_F16) -> None:
+    """Router + routed/shared experts of one MoE layer (M = 1..4 tokens)."""
+    rc = lib().wisp_gpu_moe_layer_decode_int4(router_w, router_bias or None, kind, scores, idx, w,
+                                              table, shared_blob or None, ctypes.byref(layout), x,
+                                              x_dtype, n_tokens, top_k, n_experts, ws.ptr,
+                                              ws.nbytes, 1 if accumulate else 0, out32 or None,
+                                              out16 or None, stream or None)
+    _ck(rc, "wisp_gpu_moe_layer_decode_int4")
+
+
 def moe_route(router_w: int, bias: int, x: int, n_tokens: int, hidden: int, n_experts: int,
               top_k: int, kind: int, logits: int, idx: int, w: int, stream: int = 0) -> None:
     rc = lib().wisp_gpu_moe_route(router_w, bias or None, x, n_tokens, hidden, n_experts, top_k,
