@@ -31,7 +31,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E peak
-EV_ROUTE, EV_PREP, EV_GATEUP, EV_DOWN, EV_COMBINE, EV_KINDS = 0, 1, 2, 3, 4, 7
+EV_ROUTE, EV_PREP, EV_GATEUP, EV_DOWN, EV_COMBINE, EV_PF_GATEUP, EV_PF_DOWN, EV_KINDS = \
+    0, 1, 2, 3, 4, 5, 6, 7
 
 
 def log(msg):
@@ -258,6 +259,77 @@ def measure(layer, steps, warmup):
     }
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+
+
+def measure_prefill(layer, n_tokens, steps, warmup, seed=2048):
+    """DeepSeek-V3-shape prefill grouped GEMM: n_tokens fp16 tokens, top-8
+    drawn without replacement from Zipf(1.1) over the 256 routed experts,
+    plus the shared expert; timed by HIP events on the launch stream
+    (graph replay of `steps` calls, and per-kernel events)."""
+    from wisp_amd import _lib, moe, synth
+    from wisp_amd.hip import DeviceBuffer, Event, Graph, synchronize, to_device
+    s = layer.shape
+    rng = np.random.default_rng(seed)
+    idx = synth.zipf_topk(rng, n_tokens, s.n_experts, s.top_k)
+    w = synth.route_weights(rng, n_tokens, s.top_k)
+    x = synth.make_x(rng, n_tokens, s.hidden)
+    dx, di, dw = to_device(x), to_device(idx), to_device(w)
+    a = layer.arenas[0]
+    ws = DeviceBuffer(moe.prefill_workspace_bytes(a.layout, n_tokens, s.top_k, s.n_experts, s.shared))
+    out16 = DeviceBuffer(2 * n_tokens * s.hidden)
+    st = layer.stream
+
+    def step():
+        moe.moe_prefill_int4(a.table.ptr, layer.shared_dev.ptr + 8 if s.shared else 0, a.layout,
+                             dx.ptr, n_tokens, di.ptr, dw.ptr, s.top_k, s.n_experts, ws,
+                             out16=out16.ptr, stream=st.handle)
+
+    for _ in range(warmup):
+        step()
+    synchronize()
+    graph = Graph(st, lambda: [step() for _ in range(steps)])
+    graph.launch(st)
+    synchronize()
+    e0, e1 = Event(), Event()
+    e0.record(st.handle)
+    graph.launch(st)
+    e1.record(st.handle)
+    synchronize()
+    ms = e0.elapsed_ms(e1) / steps
+    del graph
+    evs = [Event() for _ in range(2 * EV_KINDS)]
+    arr = (ctypes.c_void_p * (2 * EV_KINDS))(*[e.handle for e in evs])
+    lib = _lib.lib()
+    lib.wisp_amd_set_kernel_events(ctypes.cast(arr, ctypes.c_void_p), EV_KINDS)
+    step()
+    lib.wisp_amd_set_kernel_events(None, 0)
+    synchronize()
+    gu_ms = evs[2 * EV_PF_GATEUP].elapsed_ms(evs[2 * EV_PF_GATEUP + 1])
+    dn_ms = evs[2 * EV_PF_DOWN].elapsed_ms(evs[2 * EV_PF_DOWN + 1])
+    counts = np.bincount(idx.reshape(-1), minlength=s.n_experts)
+    pairs_routed = int(counts.sum())
+    per_pair = 3 * 2 * s.hidden * s.inter
+    flops = per_pair * (pairs_routed + (n_tokens if s.shared else 0))
+    tflops = flops / (ms * 1e-3) / 1e12
+    gu_flops = 2 * 2 * s.hidden * s.inter * (pairs_routed + (n_tokens if s.shared else 0))
+    dn_flops = 2 * s.hidden * s.inter * (pairs_routed + (n_tokens if s.shared else 0))
+    used = int((counts > 0).sum()) + (1 if s.shared else 0)
+    wbytes = used * synth.expert_bytes_no_zeros(s.inter, s.hidden, s.group_size)
+    return {
+        "ms_per_layer": round(ms, 4), "tokens": n_tokens,
+        "tokens_per_s": round(n_tokens / (ms * 1e-3), 1),
+        "flops": flops, "tflops": round(tflops, 2),
+        "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+        "weight_bytes_unique": wbytes, "weight_hbm_frac": round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "group_sizes": {"max": int(counts.max()), "median": float(np.median(counts)),
+                        "empty": int((counts == 0).sum())},
+        "kernel_ms": {"gate_up": round(gu_ms, 4), "down": round(dn_ms, 4)},
+        "gate_up_mfma_frac": round(gu_flops / (gu_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+        "down_mfma_frac": round(dn_flops / (dn_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+    }
+
+
 def copy_calibration(mib):
     """Five launches of a plain copy of `mib` MiB (source and destination
     both far larger than the Infinity Cache for mib >= 512)."""
@@ -285,6 +357,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline workload only")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the DeepSeek-V3 prefill grouped GEMM (2048 tokens)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB 5 times (byte-counter calibration)")
     args = ap.parse_args()
@@ -300,6 +374,12 @@ def main():
         sys.exit(1)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+
+    if args.prefill_only:
+        ds = Layer(synth.DSV3, 1, seed=777, n_sets=1)
+        r = measure_prefill(ds, 2048, max(2, min(args.steps, 10)), 2)
+        print(json.dumps({"deepseek-v3-prefill-2048": r}), flush=True)
         return
 
     # 4 Mixtral expert sets (3 GB) so consecutive steps stream cold weights
@@ -352,6 +432,8 @@ def main():
             key = f"deepseek-v3-decode-m{M}"
             extra[key] = measure(ds, max(20, args.steps // 2), 5)
             log(f"{key}: {extra[key]}")
+        extra["deepseek-v3-prefill-2048"] = measure_prefill(ds, 2048, 5, 2)
+        log(f"deepseek-v3 prefill: {extra['deepseek-v3-prefill-2048']}")
         result["extra"] = extra
     print(json.dumps(result), flush=True)
 

@@ -254,6 +254,43 @@ hipError_t wisp_gpu_moe_layer_decode_int4(const wisp_half* d_router_w,
                                           wisp_half* d_out_f16, hipStream_t s);
 
 /* ======================================================================= *
+ * 5. Fused int4 MoE prefill (grouped GEMM over routed token tiles)
+ *
+ *    out[t] = shared(x_t) + sum_k w[t,k] * expert_{idx[t,k]}(x_t) for any
+ *    number of tokens. The (token, slot) pairs are sorted by expert
+ *    (wisp_gpu_expert_offsets), cut into tiles of up to 128 tokens of one
+ *    expert, and each tile runs gate+up+SiLU and down as GEMMs on the
+ *    matrix cores: int4 weights are dequantised in registers to fp16
+ *    (the reference dequant, csrc/cuda/expert_loader.cu:42) and multiplied
+ *    with fp16 activations, fp32 accumulate. h and the per-pair down
+ *    outputs are fp16 in the workspace; the combine adds each token's slots
+ *    in order (shared first, then rank order), so results are
+ *    deterministic. Replaces the reference's per-token loop over
+ *    decode_step (csrc/core/wisp_engine.c:2292-2307), which re-reads every
+ *    selected expert's weights for every token.
+ * ======================================================================= */
+
+/* Workspace bytes for wisp_gpu_moe_prefill_int4 (0 for invalid sizes). */
+size_t wisp_moe_prefill_workspace_bytes(const WispExpertLayout* L,
+                                        int n_tokens, int top_k,
+                                        int n_experts, int has_shared);
+
+/* Arguments as wisp_gpu_moe_decode_int4, with any n_tokens >= 1 and fp16
+ * x (16-byte aligned). Also needs hidden % 256 == 0 and n_experts + 1 <=
+ * 1024. Returns hipErrorInvalidValue on bad arguments or a small
+ * workspace. */
+hipError_t wisp_gpu_moe_prefill_int4(const void* const* d_expert_table,
+                                     const void* d_shared_blob,
+                                     const WispExpertLayout* L,
+                                     const wisp_half* d_x, int n_tokens,
+                                     const int* d_topk_idx,
+                                     const float* d_topk_w, int top_k,
+                                     int n_experts, void* d_workspace,
+                                     size_t workspace_bytes, int accumulate,
+                                     float* d_out_f32, wisp_half* d_out_f16,
+                                     hipStream_t s);
+
+/* ======================================================================= *
  * 9. Profiling hook
  * ======================================================================= */
 

@@ -52,6 +52,11 @@ _SIGS = {
     "wisp_gpu_moe_layer_decode_int4": (c_int, [P, P, c_int, P, P, P, P, P, POINTER(WispExpertLayout),
                                                P, c_int, c_int, c_int, c_int, P, c_size_t, c_int,
                                                P, P, P]),
+    # section 5: fused prefill
+    "wisp_moe_prefill_workspace_bytes": (c_size_t, [POINTER(WispExpertLayout), c_int, c_int, c_int,
+                                                    c_int]),
+    "wisp_gpu_moe_prefill_int4": (c_int, [P, P, POINTER(WispExpertLayout), P, c_int, P, P, c_int,
+                                          c_int, P, c_size_t, c_int, P, P, P]),
     # profiling
     "wisp_amd_set_kernel_events": (None, [P, c_int]),
     "wisp_amd_version": (c_char_p, []),

@@ -442,8 +442,10 @@ __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void gateup_kernel(const Decode
     constexpr int NT = 2 * TILES;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int u = blockIdx.y;
-    if (u >= *P.n_unique) return;
+    /* both loads in one round trip (slot u < max_u always exists) */
+    const int n_u = *P.n_unique;
     const uint8_t* blob = P.ublob[u];
+    if (u >= n_u) return;
     const int K = P.hidden;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int col = lane & 15, j = lane >> 4;
@@ -550,8 +552,9 @@ __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void down_kernel(const DecodePa
     const int nch = P.n_chunks;
     const int u = blockIdx.y / nch, c = blockIdx.y - u * nch;
     const int r0 = blockIdx.x * 16 * TILES;
-    if (u >= *P.n_unique) return;
+    const int n_u = *P.n_unique;
     const uint8_t* blob = P.ublob[u];
+    if (u >= n_u) return;
     const int K = P.inter, H = P.hidden;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int col = lane & 15, j = lane >> 4;

@@ -1,0 +1,481 @@
+/*
+ * moe_prefill.hip — int4 MoE prefill as a grouped GEMM over routed token
+ * tiles on gfx950 (MFMA fp16, fp32 accumulate).
+ *
+ * The reference has no batched MoE: prefill and speculative verify call the
+ * single-token decode once per token (csrc/core/wisp_engine.c:2292-2307,
+ * 2317-2330), so every selected expert's weights are read once per token.
+ * Here every expert's weights are read once per tile of up to 128 of its
+ * tokens:
+ *
+ *   prep    : (token, slot) pairs with the shared expert as slot 0 (expert
+ *             id n_experts, weight 1), so the combine order is the
+ *             reference's: shared, then routed experts in rank order
+ *             (csrc/core/wisp_engine.c:1594-1602, 1653-1670).
+ *   offsets : wisp_gpu_expert_offsets (counting sort of the pairs by
+ *             expert, stable in flat pair order).
+ *   tiles   : one workgroup turns the expert counts into the tile list
+ *             (expert, first pair, rows <= 128).
+ *   gate/up : grid (tiles, inter/128). A wave owns 2 gate + 2 up row tiles
+ *             (16 rows each) of one expert; per 128-wide K block each lane
+ *             loads 16 B of packed nibbles per row tile (32 consecutive K
+ *             of one row), dequantises them in registers to fp16
+ *             fp16((q - 8) * s + z) (the reference dequant,
+ *             csrc/cuda/expert_loader.cu:42) and feeds them as the B operand
+ *             of v_mfma_f32_16x16x32_f16 against up to 8 16-token A tiles
+ *             gathered from x into double-buffered LDS. Sub-tiles past the
+ *             tile's token count are skipped. Epilogue:
+ *             h = w_route * silu(g) * u, fp16, in sorted pair order.
+ *   down    : same kernel shape over h (rows contiguous per expert), 4 row
+ *             tiles per wave; writes y' = down . h' (fp16) per pair.
+ *   combine : out[t] (+)= sum over the token's slots in order of y'.
+ *
+ * Weights are read in place from the reference blob layout
+ * (csrc/core/wisp_engine.h:214-238); nothing is dequantised to memory.
+ */
+#include "hip_common.h"
+
+#define PF_BM 128                 /* tokens per tile                         */
+#define PF_T (PF_BM / 16)         /* 16-token MFMA sub-tiles per tile        */
+#define PF_NT 4                   /* 16-row weight tiles per wave            */
+#define PF_WAVES 4
+#define PF_THREADS (64 * PF_WAVES)
+#define PF_AROW 136               /* LDS A row stride in halves (128 + 8)    */
+#define PF_R 3                    /* register ring: weight blocks in flight  */
+#define PF_MAX_EXPERTS 4096
+
+struct PfParams {
+    uint64_t p_off[3], s_off[3], z_off[3];
+    int hidden, inter, gs, has_zeros;
+    int n_tokens, top_k1, n_experts1, max_tiles;
+    const uint8_t** table1;   /* [n_experts1] blob pointers, shared last     */
+    int* idx1;                /* [n_tokens][top_k1] expert id per pair       */
+    float* w1;                /* [n_tokens][top_k1] routing weight per pair  */
+    int* counts;              /* [n_experts1]                                */
+    int* offsets;             /* [n_experts1 + 1]                            */
+    int* order;               /* [n_pairs] flat pair index, sorted by expert */
+    int* inv;                 /* [n_pairs] position of each pair in order    */
+    int* n_tiles;
+    int4* tiles;              /* [max_tiles] (expert, first position, rows)  */
+    uint16_t* H;              /* [n_pairs][inter] fp16 h', sorted order      */
+    uint16_t* Y;              /* [n_pairs][hidden] fp16 y', sorted order     */
+    const uint16_t* x;        /* [n_tokens][hidden] fp16                      */
+    float* out32;
+    uint16_t* out16;
+    int accumulate;
+};
+
+/* ======================================================================= */
+/* prep and tile list                                                       */
+/* ======================================================================= */
+
+/* idx1/w1: slot 0 = shared expert (id n_experts1 - 1, weight 1) when
+ * present, then the routed slots; table1 = table plus the shared blob. */
+__global__ __launch_bounds__(256) void pf_prep_kernel(PfParams P, const void* const* table,
+                                                      const void* shared_blob, const int* idx,
+                                                      const float* w, int top_k,
+                                                      int n_experts) {
+    const int sh = shared_blob ? 1 : 0;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n_experts) P.table1[i] = (const uint8_t*)table[i];
+    if (i == 0 && sh) P.table1[n_experts] = (const uint8_t*)shared_blob;
+    if (i < P.n_tokens * P.top_k1) {
+        const int t = i / P.top_k1, k = i - t * P.top_k1;
+        int e;
+        float wv;
+        if (sh && k == 0) {
+            e = n_experts;
+            wv = 1.0f;
+        } else {
+            e = idx[t * top_k + k - sh];
+            wv = w[t * top_k + k - sh];
+            if (e < 0 || e >= n_experts) e = -1;
+        }
+        P.idx1[i] = e;
+        P.w1[i] = wv;
+    }
+}
+
+/* One workgroup: tiles of up to PF_BM pairs per expert, experts in order. */
+__global__ __launch_bounds__(256) void pf_tiles_kernel(PfParams P) {
+    __shared__ int s_start[PF_MAX_EXPERTS + 1];
+    const int E = P.n_experts1;
+    if (threadIdx.x == 0) {
+        int acc = 0;
+        for (int e = 0; e < E; e++) {
+            s_start[e] = acc;
+            acc += (P.counts[e] + PF_BM - 1) / PF_BM;
+        }
+        s_start[E] = acc;
+        *P.n_tiles = acc < P.max_tiles ? acc : P.max_tiles;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        const int c = P.counts[e], o = P.offsets[e];
+        for (int q = 0, t = s_start[e]; q < c && t < P.max_tiles; q += PF_BM, t++)
+            P.tiles[t] = make_int4(e, o + q, min(PF_BM, c - q), 0);
+    }
+}
+
+/* ======================================================================= */
+/* grouped GEMM                                                             */
+/* ======================================================================= */
+
+/* 8 fp16 values e0..e7 (natural order) -> slot order e0 e4 e1 e5 e2 e6 e3 e7
+ * (the order dequant8 produces). */
+__device__ __forceinline__ u4 perm8_halves(u4 v) {
+    u4 o;
+    o.x = (v.x & 0xFFFFu) | (v.z << 16);
+    o.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
+    o.z = (v.y & 0xFFFFu) | (v.w << 16);
+    o.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
+    return o;
+}
+
+/* Two nibbles already OR-ed into fp16 1024.0 -> fp16((q - 8) * s + z):
+ * subtracting 1032 gives q - 8 exactly; one packed multiply (or fma with
+ * the zero) rounds once to fp16. */
+template <bool HZ>
+__device__ __forceinline__ uint32_t dequant2(uint32_t d, h2 s2, h2 z2) {
+    const h2 off = {(f16)1032.0f, (f16)1032.0f};
+    const h2 q = __builtin_bit_cast(h2, d) - off;
+    return __builtin_bit_cast(uint32_t, HZ ? q * s2 + z2 : q * s2);
+}
+
+/* 8 nibbles of one dword -> fp16((q - 8) * s + z) in slot order
+ * e0 e4 e1 e5 e2 e6 e3 e7. OR-ing a nibble into the mantissa of 1024.0
+ * (0x6400) gives exactly 1024 + q. Written with one scalar per dword: an
+ * element of a vector value subscripted by an unrolled loop index inside
+ * __builtin_bit_cast was folded to element 0 by this compiler. */
+template <bool HZ>
+__device__ __forceinline__ h8 dequant8(uint32_t w, h2 s2, h2 z2) {
+    const uint32_t m = 0x000F000Fu, one024 = 0x64006400u;
+    u4 o;
+    o.x = dequant2<HZ>((w & m) | one024, s2, z2);
+    o.y = dequant2<HZ>(((w >> 4) & m) | one024, s2, z2);
+    o.z = dequant2<HZ>(((w >> 8) & m) | one024, s2, z2);
+    o.w = dequant2<HZ>(((w >> 12) & m) | one024, s2, z2);
+    return __builtin_bit_cast(h8, o);
+}
+
+/* grid (max_tiles, n-blocks). GATEUP: the workgroup covers h features
+ * [128 by, 128 by + 128): wave w owns gate rows f0 .. f0 + 31 and up rows
+ * f0 .. f0 + 31 with f0 = 128 by + 32 w (row tiles s = 0,1 gate, 2,3 up).
+ * DOWN: output rows [256 by, +256): wave w owns 4 row tiles from
+ * 256 by + 64 w. K = hidden (GATEUP) or inter (DOWN), 128-wide blocks. */
+template <bool GATEUP, bool HZ>
+__global__ __launch_bounds__(PF_THREADS) void pf_gemm_kernel(const PfParams P) {
+    __shared__ __attribute__((aligned(16))) uint16_t s_a[2][PF_BM * PF_AROW];
+    __shared__ int s_row[PF_BM];      /* source row of each tile row (-1: none) */
+    __shared__ float s_wr[PF_BM];     /* routing weight of each tile row        */
+    const int tile = blockIdx.x;
+    const int n_tiles = *P.n_tiles;
+    const int4 td = P.tiles[tile < P.max_tiles ? tile : 0];
+    if (tile >= n_tiles) return;
+    const int e = td.x, p0 = td.y, nv = td.z;
+    const uint8_t* blob = P.table1[e];
+    const int K = GATEUP ? P.hidden : P.inter;
+    const int nblk = K / 128;
+    const int G = K / P.gs;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, j = lane >> 4;
+    const int tv = (nv + 15) / 16;            /* live 16-token sub-tiles */
+
+    for (int r = threadIdx.x; r < PF_BM; r += PF_THREADS) {
+        if (r < nv) {
+            const int pair = P.order[p0 + r];
+            s_row[r] = GATEUP ? pair / P.top_k1 : p0 + r;
+            s_wr[r] = P.w1[pair];
+        } else {
+            s_row[r] = -1;
+            s_wr[r] = 0.0f;
+        }
+    }
+
+    /* weight row tiles of this wave */
+    const uint8_t* wp[PF_NT];
+    const uint16_t* sp[PF_NT];
+    const uint16_t* zp[PF_NT];
+#pragma unroll
+    for (int s = 0; s < PF_NT; s++) {
+        int mat, row;
+        if (GATEUP) {
+            mat = s < 2 ? 0 : 1;
+            row = blockIdx.y * 128 + wave * 32 + 16 * (s & 1) + col;
+        } else {
+            mat = 2;
+            row = blockIdx.y * 256 + wave * 64 + 16 * s + col;
+        }
+        wp[s] = blob + P.p_off[mat] + (size_t)row * (K / 2) + 16 * j;
+        sp[s] = (const uint16_t*)(blob + P.s_off[mat]) + (size_t)row * G;
+        zp[s] = (const uint16_t*)(blob + P.z_off[mat]) + (size_t)row * G;
+    }
+    /* group of this lane's 32 K values in block b: (128 b + 32 j) / gs */
+    const int gshift = 31 - __builtin_clz(P.gs);
+
+    f4 acc[PF_T][PF_NT];
+#pragma unroll
+    for (int t = 0; t < PF_T; t++)
+#pragma unroll
+        for (int s = 0; s < PF_NT; s++) acc[t][s] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+
+    __syncthreads();   /* s_row visible */
+
+    /* A staging: tile rows x 128 K of block b, 16 B pieces, 8 per thread */
+    constexpr int APT = PF_BM * 16 / PF_THREADS;
+    const uint16_t* asrc = GATEUP ? P.x : P.H;
+    const int astride = K;
+    u4 areg[APT];
+    auto a_issue = [&](int b) {
+#pragma unroll
+        for (int c = 0; c < APT; c++) {
+            const int i = threadIdx.x + c * PF_THREADS;
+            const int r = i >> 4, q = i & 15;
+            const int src = s_row[r];
+            areg[c] = src >= 0 ? *(const u4*)(asrc + (size_t)src * astride + b * 128 + 8 * q)
+                               : (u4){0u, 0u, 0u, 0u};
+        }
+    };
+    auto a_commit = [&](int buf) {
+#pragma unroll
+        for (int c = 0; c < APT; c++) {
+            const int i = threadIdx.x + c * PF_THREADS;
+            const int r = i >> 4, q = i & 15;
+            *(u4*)(&s_a[buf][r * PF_AROW + 8 * q]) = perm8_halves(areg[c]);
+        }
+    };
+
+    /* weight ring: block b lives in slot b % PF_R */
+    u4 wr[PF_R][PF_NT];
+    uint16_t sr[PF_R][PF_NT], zr[PF_R][PF_NT];
+    auto w_issue = [&](int slot, int b) {
+        const int bb = min(b, nblk - 1);
+        const int g = (bb * 128 + 32 * j) >> gshift;
+#pragma unroll
+        for (int s = 0; s < PF_NT; s++) {
+            wr[slot][s] = *(const u4*)(wp[s] + (size_t)bb * 64);
+            sr[slot][s] = sp[s][g];
+            if (HZ) zr[slot][s] = zp[s][g];
+        }
+    };
+
+    a_issue(0);
+#pragma unroll
+    for (int r = 0; r < PF_R - 1; r++) w_issue(r, r);
+    a_commit(0);
+    __syncthreads();
+
+    for (int b0 = 0; b0 < nblk; b0 += PF_R) {
+#pragma unroll
+        for (int r = 0; r < PF_R; r++) {
+            const int b = b0 + r;
+            if (b < nblk) {
+                w_issue((r + PF_R - 1) % PF_R, b + PF_R - 1);
+                const bool more = b + 1 < nblk;
+                if (more) a_issue(b + 1);
+                const uint16_t* abuf = &s_a[b & 1][0];
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++) {
+                    h8 bf[PF_NT];
+#pragma unroll
+                    for (int s = 0; s < PF_NT; s++) {
+                        const f16 sc = __builtin_bit_cast(f16, sr[r][s]);
+                        const f16 zc = HZ ? __builtin_bit_cast(f16, zr[r][s]) : (f16)0.0f;
+                        bf[s] = dequant8<HZ>(wr[r][s][kk], (h2){sc, sc}, (h2){zc, zc});
+                    }
+#pragma unroll
+                    for (int t = 0; t < PF_T; t++) {
+                        if (t < tv) {
+                            const h8 af = *(const h8*)(abuf + (16 * t + col) * PF_AROW + 32 * j + 8 * kk);
+#pragma unroll
+                            for (int s = 0; s < PF_NT; s++) acc[t][s] = mfma16x16x32(af, bf[s], acc[t][s]);
+                        }
+                    }
+                }
+                if (more) a_commit((b + 1) & 1);
+                __syncthreads();
+            }
+        }
+    }
+
+    /* epilogue: lane holds D[4 (l/16) + v][l % 16] of each 16 x 16 tile */
+#pragma unroll
+    for (int t = 0; t < PF_T; t++) {
+        if (t < tv) {
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int r = 16 * t + 4 * j + v;
+                if (r < nv) {
+                    if (GATEUP) {
+                        const float wrt = s_wr[r];
+#pragma unroll
+                        for (int s = 0; s < 2; s++) {
+                            const float g = acc[t][s][v], u = acc[t][2 + s][v];
+                            const float h = silu_f(g) * u * wrt;
+                            const int c = blockIdx.y * 128 + wave * 32 + 16 * s + col;
+                            P.H[(size_t)(p0 + r) * P.inter + c] = __builtin_bit_cast(uint16_t, (f16)h);
+                        }
+                    } else {
+#pragma unroll
+                        for (int s = 0; s < PF_NT; s++) {
+                            const int c = blockIdx.y * 256 + wave * 64 + 16 * s + col;
+                            P.Y[(size_t)(p0 + r) * P.hidden + c] =
+                                __builtin_bit_cast(uint16_t, (f16)acc[t][s][v]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+/* out[t][c] (+)= sum over slots k (in order) of y'[inv[t * top_k1 + k]][c]. */
+__global__ __launch_bounds__(256) void pf_combine_kernel(const PfParams P) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t n = (size_t)P.n_tokens * P.hidden;
+    if (i >= n) return;
+    const int t = (int)(i / P.hidden), c = (int)(i - (size_t)t * P.hidden);
+    float y = 0.0f;
+    for (int k = 0; k < P.top_k1; k++) {
+        const int p = P.inv[t * P.top_k1 + k];
+        if (p >= 0) y += half_bits_to_float(P.Y[(size_t)p * P.hidden + c]);
+    }
+    if (P.out32) {
+        if (P.accumulate) y += P.out32[i];
+        P.out32[i] = y;
+    }
+    if (P.out16) P.out16[i] = __builtin_bit_cast(uint16_t, (f16)y);
+}
+
+/* ======================================================================= */
+/* host side                                                                */
+/* ======================================================================= */
+
+struct PfWs {
+    size_t table1, idx1, w1, counts, offsets, order, inv, ntiles, tiles, H, Y, total;
+    int max_tiles;
+};
+
+static PfWs pf_ws_layout(const WispExpertLayout* L, int n_tokens, int top_k, int n_experts,
+                         int has_shared) {
+    PfWs w;
+    const size_t k1 = (size_t)top_k + (has_shared ? 1 : 0);
+    const size_t e1 = (size_t)n_experts + (has_shared ? 1 : 0);
+    const size_t np = (size_t)n_tokens * k1;
+    w.max_tiles = (int)((np + PF_BM - 1) / PF_BM + e1);
+    size_t off = 0;
+    w.table1 = off; off = align_up(off + e1 * sizeof(void*), 256);
+    w.idx1 = off; off = align_up(off + np * 4, 256);
+    w.w1 = off; off = align_up(off + np * 4, 256);
+    w.counts = off; off = align_up(off + e1 * 4, 256);
+    w.offsets = off; off = align_up(off + (e1 + 1) * 4, 256);
+    w.order = off; off = align_up(off + np * 4, 256);
+    w.inv = off; off = align_up(off + np * 4, 256);
+    w.ntiles = off; off = align_up(off + 4, 256);
+    w.tiles = off; off = align_up(off + (size_t)w.max_tiles * 16, 256);
+    w.H = off; off = align_up(off + np * L->rows[0] * 2, 256);
+    w.Y = off; off = align_up(off + np * L->cols[0] * 2, 256);
+    w.total = off;
+    return w;
+}
+
+static bool pf_shape_ok(const WispExpertLayout* L) {
+    if (wisp_expert_layout_check(L) != hipSuccess) return false;
+    const uint32_t inter = L->rows[0], hidden = L->cols[0];
+    /* gate/up n-blocks of 128 h features, down n-blocks of 256 rows, group
+     * size a power of two >= 32 (one scale per lane's 32 K values) */
+    return inter % 128 == 0 && hidden % 256 == 0 && L->group_size >= 32;
+}
+
+extern "C" size_t wisp_moe_prefill_workspace_bytes(const WispExpertLayout* L, int n_tokens,
+                                                   int top_k, int n_experts, int has_shared) {
+    if (!L || n_tokens < 1 || top_k < 1 || n_experts < 1 || n_experts + 1 > PF_MAX_EXPERTS)
+        return 0;
+    return pf_ws_layout(L, n_tokens, top_k, n_experts, has_shared).total;
+}
+
+extern "C" hipError_t wisp_gpu_expert_offsets(const int* d_topk_idx, int n_tokens, int top_k,
+                                              int n_experts, int* d_counts, int* d_offsets,
+                                              int* d_order, int* d_inv, hipStream_t s);
+
+extern "C" hipError_t wisp_gpu_moe_prefill_int4(const void* const* d_expert_table,
+                                                const void* d_shared_blob,
+                                                const WispExpertLayout* L, const wisp_half* d_x,
+                                                int n_tokens, const int* d_topk_idx,
+                                                const float* d_topk_w, int top_k, int n_experts,
+                                                void* d_workspace, size_t workspace_bytes,
+                                                int accumulate, float* d_out_f32,
+                                                wisp_half* d_out_f16, hipStream_t s) {
+    if (!L || n_tokens < 1 || top_k < 1 || n_experts < 1 || n_experts + 1 > PF_MAX_EXPERTS ||
+        !d_expert_table || !d_x || !d_topk_idx || !d_topk_w || !d_workspace ||
+        (!d_out_f32 && !d_out_f16) || ((uintptr_t)d_x % 16))
+        return hipErrorInvalidValue;
+    if (!pf_shape_ok(L)) return hipErrorInvalidValue;
+    const int sh = d_shared_blob ? 1 : 0;
+    const PfWs w = pf_ws_layout(L, n_tokens, top_k, n_experts, sh);
+    if (workspace_bytes < w.total) return hipErrorInvalidValue;
+    if ((long)n_tokens * (top_k + sh) > (1L << 30)) return hipErrorInvalidValue;
+
+    PfParams P;
+    for (int m = 0; m < 3; m++) {
+        P.p_off[m] = L->packed_off[m];
+        P.s_off[m] = L->scales_off[m];
+        P.z_off[m] = L->zeros_off[m];
+    }
+    P.hidden = (int)L->cols[0];
+    P.inter = (int)L->rows[0];
+    P.gs = (int)L->group_size;
+    P.has_zeros = L->has_zeros ? 1 : 0;
+    P.n_tokens = n_tokens;
+    P.top_k1 = top_k + sh;
+    P.n_experts1 = n_experts + sh;
+    P.max_tiles = w.max_tiles;
+    char* ws = (char*)d_workspace;
+    P.table1 = (const uint8_t**)(ws + w.table1);
+    P.idx1 = (int*)(ws + w.idx1);
+    P.w1 = (float*)(ws + w.w1);
+    P.counts = (int*)(ws + w.counts);
+    P.offsets = (int*)(ws + w.offsets);
+    P.order = (int*)(ws + w.order);
+    P.inv = (int*)(ws + w.inv);
+    P.n_tiles = (int*)(ws + w.ntiles);
+    P.tiles = (int4*)(ws + w.tiles);
+    P.H = (uint16_t*)(ws + w.H);
+    P.Y = (uint16_t*)(ws + w.Y);
+    P.x = (const uint16_t*)d_x;
+    P.out32 = d_out_f32;
+    P.out16 = (uint16_t*)d_out_f16;
+    P.accumulate = accumulate ? 1 : 0;
+
+    const int n_pairs = n_tokens * P.top_k1;
+    const int prep_n = n_pairs > n_experts ? n_pairs : n_experts;
+    hipLaunchKernelGGL(pf_prep_kernel, dim3((prep_n + 255) / 256), dim3(256), 0, s, P,
+                       d_expert_table, d_shared_blob, d_topk_idx, d_topk_w, top_k, n_experts);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    e = wisp_gpu_expert_offsets(P.idx1, n_tokens, P.top_k1, P.n_experts1, P.counts, P.offsets,
+                                P.order, P.inv, s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(pf_tiles_kernel, dim3(1), dim3(256), 0, s, P);
+    const bool hz = P.has_zeros != 0;
+    ev_before(EV_PF_GATEUP, s);
+    if (hz)
+        hipLaunchKernelGGL((pf_gemm_kernel<true, true>), dim3(P.max_tiles, P.inter / 128),
+                           dim3(PF_THREADS), 0, s, P);
+    else
+        hipLaunchKernelGGL((pf_gemm_kernel<true, false>), dim3(P.max_tiles, P.inter / 128),
+                           dim3(PF_THREADS), 0, s, P);
+    ev_after(EV_PF_GATEUP, s);
+    ev_before(EV_PF_DOWN, s);
+    if (hz)
+        hipLaunchKernelGGL((pf_gemm_kernel<false, true>), dim3(P.max_tiles, P.hidden / 256),
+                           dim3(PF_THREADS), 0, s, P);
+    else
+        hipLaunchKernelGGL((pf_gemm_kernel<false, false>), dim3(P.max_tiles, P.hidden / 256),
+                           dim3(PF_THREADS), 0, s, P);
+    ev_after(EV_PF_DOWN, s);
+    const size_t n_out = (size_t)n_tokens * P.hidden;
+    hipLaunchKernelGGL(pf_combine_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, s,
+                       P);
+    return hipGetLastError();
+}

@@ -101,6 +101,24 @@ def moe_layer_decode_int4(router_w: int, router_bias: int, kind: int, scores: in
     _ck(rc, "wisp_gpu_moe_layer_decode_int4")
 
 
+def prefill_workspace_bytes(layout: WispExpertLayout, n_tokens: int, top_k: int, n_experts: int,
+                            has_shared: bool) -> int:
+    return int(lib().wisp_moe_prefill_workspace_bytes(ctypes.byref(layout), n_tokens, top_k,
+                                                       n_experts, 1 if has_shared else 0))
+
+
+def moe_prefill_int4(table: int, shared_blob: int, layout: WispExpertLayout, x: int,
+                     n_tokens: int, topk_idx: int, topk_w: int, top_k: int, n_experts: int,
+                     ws: DeviceBuffer, out32: int = 0, out16: int = 0, stream: int = 0,
+                     accumulate: bool = False) -> None:
+    """Grouped-GEMM MoE over any number of tokens (fp16 x)."""
+    rc = lib().wisp_gpu_moe_prefill_int4(table, shared_blob or None, ctypes.byref(layout), x,
+                                         n_tokens, topk_idx, topk_w, top_k, n_experts, ws.ptr,
+                                         ws.nbytes, 1 if accumulate else 0, out32 or None,
+                                         out16 or None, stream or None)
+    _ck(rc, "wisp_gpu_moe_prefill_int4")
+
+
 def moe_route(router_w: int, bias: int, x: int, n_tokens: int, hidden: int, n_experts: int,
               top_k: int, kind: int, logits: int, idx: int, w: int, stream: int = 0) -> None:
     rc = lib().wisp_gpu_moe_route(router_w, bias or None, x, n_tokens, hidden, n_experts, top_k,
