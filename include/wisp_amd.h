@@ -275,9 +275,9 @@ size_t wisp_moe_prefill_workspace_bytes(const WispExpertLayout* L,
                                         int n_tokens, int top_k,
                                         int n_experts, int has_shared);
 
-/* Arguments as wisp_gpu_moe_decode_int4, with any n_tokens >= 1 and fp16
- * x (16-byte aligned). Also needs hidden % 256 == 0 and n_experts + 1 <=
- * 1024. Returns hipErrorInvalidValue on bad arguments or a small
+/* Arguments as wisp_gpu_moe_decode_int4, with any n_tokens >= 1, fp16 x
+ * and 16-byte aligned x and outputs. Also needs hidden % 256 == 0 and
+ * n_experts + 1 <= 1024. Returns hipErrorInvalidValue on bad arguments or a small
  * workspace. */
 hipError_t wisp_gpu_moe_prefill_int4(const void* const* d_expert_table,
                                      const void* d_shared_blob,

@@ -36,13 +36,12 @@
 #include "hip_common.h"
 
 #define PF_BM 128                 /* tokens per tile                         */
-#define PF_T (PF_BM / 16)         /* 16-token MFMA sub-tiles per tile        */
 #define PF_NT 4                   /* 16-row weight tiles per wave            */
 #define PF_WAVES 4
 #define PF_THREADS (64 * PF_WAVES)
 #define PF_AROW 136               /* LDS A row stride in halves (128 + 8)    */
-#define PF_R 3                    /* register ring: weight blocks in flight  */
 #define PF_MAX_EXPERTS 4096
+#define PF_CLASSES 3              /* tiles of <= 32, <= 64, <= 128 tokens    */
 
 struct PfParams {
     uint64_t p_off[3], s_off[3], z_off[3];
@@ -55,8 +54,8 @@ struct PfParams {
     int* offsets;             /* [n_experts1 + 1]                            */
     int* order;               /* [n_pairs] flat pair index, sorted by expert */
     int* inv;                 /* [n_pairs] position of each pair in order    */
-    int* n_tiles;
-    int4* tiles;              /* [max_tiles] (expert, first position, rows)  */
+    int* n_tiles;             /* [PF_CLASSES]                                */
+    int4* tiles;              /* [PF_CLASSES][max_tiles] (expert, first position, rows) */
     uint16_t* H;              /* [n_pairs][inter] fp16 h', sorted order      */
     uint16_t* Y;              /* [n_pairs][hidden] fp16 y', sorted order     */
     const uint16_t* x;        /* [n_tokens][hidden] fp16                      */
@@ -96,25 +95,33 @@ __global__ __launch_bounds__(256) void pf_prep_kernel(PfParams P, const void* co
     }
 }
 
-/* One workgroup: tiles of up to PF_BM pairs per expert, experts in order. */
+/* Tile class of a tile with `rows` tokens: its compile-time count of
+ * 16-token sub-tiles is 2, 4 or 8. */
+__host__ __device__ inline int pf_class(int rows) { return rows <= 32 ? 0 : (rows <= 64 ? 1 : 2); }
+
+/* One workgroup: tiles of up to PF_BM pairs per expert, experts in order,
+ * appended to the list of their class (tiles[c * max_tiles + i]). The
+ * counts and offsets are read into LDS by all threads first; one thread
+ * then walks them. */
 __global__ __launch_bounds__(256) void pf_tiles_kernel(PfParams P) {
-    __shared__ int s_start[PF_MAX_EXPERTS + 1];
+    __shared__ int s_cnt[PF_MAX_EXPERTS], s_off[PF_MAX_EXPERTS];
     const int E = P.n_experts1;
-    if (threadIdx.x == 0) {
-        int acc = 0;
-        for (int e = 0; e < E; e++) {
-            s_start[e] = acc;
-            acc += (P.counts[e] + PF_BM - 1) / PF_BM;
-        }
-        s_start[E] = acc;
-        *P.n_tiles = acc < P.max_tiles ? acc : P.max_tiles;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        s_cnt[e] = P.counts[e];
+        s_off[e] = P.offsets[e];
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        const int c = P.counts[e], o = P.offsets[e];
-        for (int q = 0, t = s_start[e]; q < c && t < P.max_tiles; q += PF_BM, t++)
-            P.tiles[t] = make_int4(e, o + q, min(PF_BM, c - q), 0);
+    if (threadIdx.x != 0) return;
+    int n[PF_CLASSES] = {0, 0, 0};
+    for (int e = 0; e < E; e++) {
+        const int c = s_cnt[e], o = s_off[e];
+        for (int q = 0; q < c; q += PF_BM) {
+            const int rows = min(PF_BM, c - q);
+            const int k = pf_class(rows);
+            if (n[k] < P.max_tiles) P.tiles[k * P.max_tiles + n[k]++] = make_int4(e, o + q, rows, 0);
+        }
     }
+    for (int k = 0; k < PF_CLASSES; k++) P.n_tiles[k] = n[k];
 }
 
 /* ======================================================================= */
@@ -158,19 +165,28 @@ __device__ __forceinline__ h8 dequant8(uint32_t w, h2 s2, h2 z2) {
     return __builtin_bit_cast(h8, o);
 }
 
-/* grid (max_tiles, n-blocks). GATEUP: the workgroup covers h features
- * [128 by, 128 by + 128): wave w owns gate rows f0 .. f0 + 31 and up rows
- * f0 .. f0 + 31 with f0 = 128 by + 32 w (row tiles s = 0,1 gate, 2,3 up).
- * DOWN: output rows [256 by, +256): wave w owns 4 row tiles from
- * 256 by + 64 w. K = hidden (GATEUP) or inter (DOWN), 128-wide blocks. */
-template <bool GATEUP, bool HZ>
-__global__ __launch_bounds__(PF_THREADS) void pf_gemm_kernel(const PfParams P) {
-    __shared__ __attribute__((aligned(16))) uint16_t s_a[2][PF_BM * PF_AROW];
-    __shared__ int s_row[PF_BM];      /* source row of each tile row (-1: none) */
-    __shared__ float s_wr[PF_BM];     /* routing weight of each tile row        */
+/* grid (tiles of class CLS, n-blocks). GATEUP: the workgroup covers h
+ * features [128 by, 128 by + 128): wave w owns gate rows f0 .. f0 + 31 and
+ * up rows f0 .. f0 + 31 with f0 = 128 by + 32 w (row tiles s = 0,1 gate,
+ * 2,3 up). DOWN: output rows [256 by, +256): wave w owns 4 row tiles from
+ * 256 by + 64 w. K = hidden (GATEUP) or inter (DOWN) in 128-wide blocks.
+ * TV: 16-token sub-tiles of the class (rows past the tile's count are
+ * zeros); R: weight blocks held in the register ring (R - 1 in flight
+ * while one is computed).
+ *
+ * Pipeline of step b: commit the A tile of block b + 1 (loaded during step
+ * b - 1) to the other LDS buffer, issue the A loads of block b + 2, issue
+ * the weights of block b + R - 1, compute block b, barrier. */
+template <bool GATEUP, bool HZ, int TV, int R>
+__global__ __launch_bounds__(PF_THREADS) void pf_gemm_kernel(const PfParams P, int cls) {
+    constexpr int BM = 16 * TV;
+    constexpr int APT = BM * 16 / PF_THREADS;   /* A pieces (16 B) per thread per block */
+    __shared__ __attribute__((aligned(16))) uint16_t s_a[2][BM * PF_AROW];
+    __shared__ int s_row[BM];      /* source row of each tile row (-1: none) */
+    __shared__ float s_wr[BM];     /* routing weight of each tile row        */
     const int tile = blockIdx.x;
-    const int n_tiles = *P.n_tiles;
-    const int4 td = P.tiles[tile < P.max_tiles ? tile : 0];
+    const int n_tiles = P.n_tiles[cls];
+    const int4 td = P.tiles[cls * P.max_tiles + tile];
     if (tile >= n_tiles) return;
     const int e = td.x, p0 = td.y, nv = td.z;
     const uint8_t* blob = P.table1[e];
@@ -179,9 +195,8 @@ __global__ __launch_bounds__(PF_THREADS) void pf_gemm_kernel(const PfParams P) {
     const int G = K / P.gs;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, j = lane >> 4;
-    const int tv = (nv + 15) / 16;            /* live 16-token sub-tiles */
 
-    for (int r = threadIdx.x; r < PF_BM; r += PF_THREADS) {
+    for (int r = threadIdx.x; r < BM; r += PF_THREADS) {
         if (r < nv) {
             const int pair = P.order[p0 + r];
             s_row[r] = GATEUP ? pair / P.top_k1 : p0 + r;
@@ -213,41 +228,41 @@ __global__ __launch_bounds__(PF_THREADS) void pf_gemm_kernel(const PfParams P) {
     /* group of this lane's 32 K values in block b: (128 b + 32 j) / gs */
     const int gshift = 31 - __builtin_clz(P.gs);
 
-    f4 acc[PF_T][PF_NT];
+    f4 acc[TV][PF_NT];
 #pragma unroll
-    for (int t = 0; t < PF_T; t++)
+    for (int t = 0; t < TV; t++)
 #pragma unroll
         for (int s = 0; s < PF_NT; s++) acc[t][s] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
 
     __syncthreads();   /* s_row visible */
 
-    /* A staging: tile rows x 128 K of block b, 16 B pieces, 8 per thread */
-    constexpr int APT = PF_BM * 16 / PF_THREADS;
+    /* A staging: BM rows x 128 K of a block, 16 B pieces */
     const uint16_t* asrc = GATEUP ? P.x : P.H;
-    const int astride = K;
     u4 areg[APT];
+    int aoff[APT];     /* element offset of each piece's source row (-1: zero) */
+#pragma unroll
+    for (int c = 0; c < APT; c++) {
+        const int i = threadIdx.x + c * PF_THREADS;
+        const int src = s_row[i >> 4];
+        aoff[c] = src >= 0 ? src * K + 8 * (i & 15) : -1;
+    }
     auto a_issue = [&](int b) {
 #pragma unroll
-        for (int c = 0; c < APT; c++) {
-            const int i = threadIdx.x + c * PF_THREADS;
-            const int r = i >> 4, q = i & 15;
-            const int src = s_row[r];
-            areg[c] = src >= 0 ? *(const u4*)(asrc + (size_t)src * astride + b * 128 + 8 * q)
-                               : (u4){0u, 0u, 0u, 0u};
-        }
+        for (int c = 0; c < APT; c++)
+            areg[c] = aoff[c] >= 0 ? *(const u4*)(asrc + (size_t)aoff[c] + b * 128)
+                                   : (u4){0u, 0u, 0u, 0u};
     };
     auto a_commit = [&](int buf) {
 #pragma unroll
         for (int c = 0; c < APT; c++) {
             const int i = threadIdx.x + c * PF_THREADS;
-            const int r = i >> 4, q = i & 15;
-            *(u4*)(&s_a[buf][r * PF_AROW + 8 * q]) = perm8_halves(areg[c]);
+            *(u4*)(&s_a[buf][(i >> 4) * PF_AROW + 8 * (i & 15)]) = perm8_halves(areg[c]);
         }
     };
 
-    /* weight ring: block b lives in slot b % PF_R */
-    u4 wr[PF_R][PF_NT];
-    uint16_t sr[PF_R][PF_NT], zr[PF_R][PF_NT];
+    /* weight ring: block b lives in slot b % R */
+    u4 wr[R][PF_NT];
+    uint16_t sr[R][PF_NT], zr[R][PF_NT];
     auto w_issue = [&](int slot, int b) {
         const int bb = min(b, nblk - 1);
         const int g = (bb * 128 + 32 * j) >> gshift;
@@ -260,39 +275,36 @@ __global__ __launch_bounds__(PF_THREADS) void pf_gemm_kernel(const PfParams P) {
     };
 
     a_issue(0);
-#pragma unroll
-    for (int r = 0; r < PF_R - 1; r++) w_issue(r, r);
     a_commit(0);
+    if (nblk > 1) a_issue(1);
+#pragma unroll
+    for (int r = 0; r < R - 1; r++) w_issue(r, r);
     __syncthreads();
 
-    for (int b0 = 0; b0 < nblk; b0 += PF_R) {
+    for (int b0 = 0; b0 < nblk; b0 += R) {
 #pragma unroll
-        for (int r = 0; r < PF_R; r++) {
+        for (int r = 0; r < R; r++) {
             const int b = b0 + r;
             if (b < nblk) {
-                w_issue((r + PF_R - 1) % PF_R, b + PF_R - 1);
-                const bool more = b + 1 < nblk;
-                if (more) a_issue(b + 1);
+                if (b + 1 < nblk) a_commit((b + 1) & 1);
+                if (b + 2 < nblk) a_issue(b + 2);
+                w_issue((r + R - 1) % R, b + R - 1);
                 const uint16_t* abuf = &s_a[b & 1][0];
 #pragma unroll
                 for (int kk = 0; kk < 4; kk++) {
-                    h8 bf[PF_NT];
+                    h8 af[TV];
+#pragma unroll
+                    for (int t = 0; t < TV; t++)
+                        af[t] = *(const h8*)(abuf + (16 * t + col) * PF_AROW + 32 * j + 8 * kk);
 #pragma unroll
                     for (int s = 0; s < PF_NT; s++) {
                         const f16 sc = __builtin_bit_cast(f16, sr[r][s]);
                         const f16 zc = HZ ? __builtin_bit_cast(f16, zr[r][s]) : (f16)0.0f;
-                        bf[s] = dequant8<HZ>(wr[r][s][kk], (h2){sc, sc}, (h2){zc, zc});
-                    }
+                        const h8 bf = dequant8<HZ>(wr[r][s][kk], (h2){sc, sc}, (h2){zc, zc});
 #pragma unroll
-                    for (int t = 0; t < PF_T; t++) {
-                        if (t < tv) {
-                            const h8 af = *(const h8*)(abuf + (16 * t + col) * PF_AROW + 32 * j + 8 * kk);
-#pragma unroll
-                            for (int s = 0; s < PF_NT; s++) acc[t][s] = mfma16x16x32(af, bf[s], acc[t][s]);
-                        }
+                        for (int t = 0; t < TV; t++) acc[t][s] = mfma16x16x32(af[t], bf, acc[t][s]);
                     }
                 }
-                if (more) a_commit((b + 1) & 1);
                 __syncthreads();
             }
         }
@@ -300,28 +312,26 @@ __global__ __launch_bounds__(PF_THREADS) void pf_gemm_kernel(const PfParams P) {
 
     /* epilogue: lane holds D[4 (l/16) + v][l % 16] of each 16 x 16 tile */
 #pragma unroll
-    for (int t = 0; t < PF_T; t++) {
-        if (t < tv) {
+    for (int t = 0; t < TV; t++) {
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int r = 16 * t + 4 * j + v;
-                if (r < nv) {
-                    if (GATEUP) {
-                        const float wrt = s_wr[r];
+        for (int v = 0; v < 4; v++) {
+            const int r = 16 * t + 4 * j + v;
+            if (r < nv) {
+                if (GATEUP) {
+                    const float wrt = s_wr[r];
 #pragma unroll
-                        for (int s = 0; s < 2; s++) {
-                            const float g = acc[t][s][v], u = acc[t][2 + s][v];
-                            const float h = silu_f(g) * u * wrt;
-                            const int c = blockIdx.y * 128 + wave * 32 + 16 * s + col;
-                            P.H[(size_t)(p0 + r) * P.inter + c] = __builtin_bit_cast(uint16_t, (f16)h);
-                        }
-                    } else {
+                    for (int s = 0; s < 2; s++) {
+                        const float g = acc[t][s][v], u = acc[t][2 + s][v];
+                        const float h = silu_f(g) * u * wrt;
+                        const int c = blockIdx.y * 128 + wave * 32 + 16 * s + col;
+                        P.H[(size_t)(p0 + r) * P.inter + c] = __builtin_bit_cast(uint16_t, (f16)h);
+                    }
+                } else {
 #pragma unroll
-                        for (int s = 0; s < PF_NT; s++) {
-                            const int c = blockIdx.y * 256 + wave * 64 + 16 * s + col;
-                            P.Y[(size_t)(p0 + r) * P.hidden + c] =
-                                __builtin_bit_cast(uint16_t, (f16)acc[t][s][v]);
-                        }
+                    for (int s = 0; s < PF_NT; s++) {
+                        const int c = blockIdx.y * 256 + wave * 64 + 16 * s + col;
+                        P.Y[(size_t)(p0 + r) * P.hidden + c] =
+                            __builtin_bit_cast(uint16_t, (f16)acc[t][s][v]);
                     }
                 }
             }
@@ -329,22 +339,38 @@ __global__ __launch_bounds__(PF_THREADS) void pf_gemm_kernel(const PfParams P) {
     }
 }
 
-/* out[t][c] (+)= sum over slots k (in order) of y'[inv[t * top_k1 + k]][c]. */
+/* out[t][c] (+)= sum over slots k (in order) of y'[inv[t * top_k1 + k]][c];
+ * 8 columns per thread with 16-byte loads (hidden % 256 == 0). */
 __global__ __launch_bounds__(256) void pf_combine_kernel(const PfParams P) {
+    const int c8 = P.hidden / 8;
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const size_t n = (size_t)P.n_tokens * P.hidden;
-    if (i >= n) return;
-    const int t = (int)(i / P.hidden), c = (int)(i - (size_t)t * P.hidden);
-    float y = 0.0f;
+    if (i >= (size_t)P.n_tokens * c8) return;
+    const int t = (int)(i / c8), c = 8 * (int)(i - (size_t)t * c8);
+    float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int k = 0; k < P.top_k1; k++) {
         const int p = P.inv[t * P.top_k1 + k];
-        if (p >= 0) y += half_bits_to_float(P.Y[(size_t)p * P.hidden + c]);
+        if (p >= 0) {
+            const h8 v = *(const h8*)(P.Y + (size_t)p * P.hidden + c);
+#pragma unroll
+            for (int q = 0; q < 8; q++) y[q] += (float)v[q];
+        }
     }
+    const size_t o = (size_t)t * P.hidden + c;
     if (P.out32) {
-        if (P.accumulate) y += P.out32[i];
-        P.out32[i] = y;
+        if (P.accumulate) {
+            const f4 a = *(const f4*)(P.out32 + o), b = *(const f4*)(P.out32 + o + 4);
+#pragma unroll
+            for (int q = 0; q < 4; q++) { y[q] += a[q]; y[4 + q] += b[q]; }
+        }
+        *(f4*)(P.out32 + o) = (f4){y[0], y[1], y[2], y[3]};
+        *(f4*)(P.out32 + o + 4) = (f4){y[4], y[5], y[6], y[7]};
     }
-    if (P.out16) P.out16[i] = __builtin_bit_cast(uint16_t, (f16)y);
+    if (P.out16) {
+        h8 h;
+#pragma unroll
+        for (int q = 0; q < 8; q++) h[q] = (f16)y[q];
+        *(h8*)(P.out16 + o) = h;
+    }
 }
 
 /* ======================================================================= */
@@ -371,8 +397,8 @@ static PfWs pf_ws_layout(const WispExpertLayout* L, int n_tokens, int top_k, int
     w.offsets = off; off = align_up(off + (e1 + 1) * 4, 256);
     w.order = off; off = align_up(off + np * 4, 256);
     w.inv = off; off = align_up(off + np * 4, 256);
-    w.ntiles = off; off = align_up(off + 4, 256);
-    w.tiles = off; off = align_up(off + (size_t)w.max_tiles * 16, 256);
+    w.ntiles = off; off = align_up(off + PF_CLASSES * 4, 256);
+    w.tiles = off; off = align_up(off + (size_t)PF_CLASSES * w.max_tiles * 16, 256);
     w.H = off; off = align_up(off + np * L->rows[0] * 2, 256);
     w.Y = off; off = align_up(off + np * L->cols[0] * 2, 256);
     w.total = off;
@@ -394,6 +420,20 @@ extern "C" size_t wisp_moe_prefill_workspace_bytes(const WispExpertLayout* L, in
     return pf_ws_layout(L, n_tokens, top_k, n_experts, has_shared).total;
 }
 
+/* One launch per tile class (sub-tiles per tile 2 / 4 / 8, weight ring
+ * 6 / 4 / 3 blocks: the memory-bound small tiles keep more weight blocks in
+ * flight, the MFMA-bound large ones spend the registers on accumulators). */
+template <bool GATEUP, bool HZ>
+static void pf_launch(const PfParams& P, const int* gx, hipStream_t s) {
+    const int ny = GATEUP ? P.inter / 128 : P.hidden / 256;
+    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 8, 3>), dim3(gx[2], ny), dim3(PF_THREADS), 0, s,
+                       P, 2);
+    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 4, 4>), dim3(gx[1], ny), dim3(PF_THREADS), 0, s,
+                       P, 1);
+    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 2, 6>), dim3(gx[0], ny), dim3(PF_THREADS), 0, s,
+                       P, 0);
+}
+
 extern "C" hipError_t wisp_gpu_expert_offsets(const int* d_topk_idx, int n_tokens, int top_k,
                                               int n_experts, int* d_counts, int* d_offsets,
                                               int* d_order, int* d_inv, hipStream_t s);
@@ -408,7 +448,8 @@ extern "C" hipError_t wisp_gpu_moe_prefill_int4(const void* const* d_expert_tabl
                                                 wisp_half* d_out_f16, hipStream_t s) {
     if (!L || n_tokens < 1 || top_k < 1 || n_experts < 1 || n_experts + 1 > PF_MAX_EXPERTS ||
         !d_expert_table || !d_x || !d_topk_idx || !d_topk_w || !d_workspace ||
-        (!d_out_f32 && !d_out_f16) || ((uintptr_t)d_x % 16))
+        (!d_out_f32 && !d_out_f16) || ((uintptr_t)d_x % 16) || ((uintptr_t)d_out_f32 % 16) ||
+        ((uintptr_t)d_out_f16 % 16))
         return hipErrorInvalidValue;
     if (!pf_shape_ok(L)) return hipErrorInvalidValue;
     const int sh = d_shared_blob ? 1 : 0;
@@ -458,23 +499,19 @@ extern "C" hipError_t wisp_gpu_moe_prefill_int4(const void* const* d_expert_tabl
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(pf_tiles_kernel, dim3(1), dim3(256), 0, s, P);
     const bool hz = P.has_zeros != 0;
+    /* grid.x per class: an upper bound on its tile count */
+    const int np = n_tokens * P.top_k1;
+    int gx[PF_CLASSES] = {P.n_experts1, np / 33 + P.n_experts1, np / 65 + P.n_experts1};
+    for (int k = 0; k < PF_CLASSES; k++) gx[k] = gx[k] < P.max_tiles ? gx[k] : P.max_tiles;
     ev_before(EV_PF_GATEUP, s);
-    if (hz)
-        hipLaunchKernelGGL((pf_gemm_kernel<true, true>), dim3(P.max_tiles, P.inter / 128),
-                           dim3(PF_THREADS), 0, s, P);
-    else
-        hipLaunchKernelGGL((pf_gemm_kernel<true, false>), dim3(P.max_tiles, P.inter / 128),
-                           dim3(PF_THREADS), 0, s, P);
+    if (hz) pf_launch<true, true>(P, gx, s);
+    else pf_launch<true, false>(P, gx, s);
     ev_after(EV_PF_GATEUP, s);
     ev_before(EV_PF_DOWN, s);
-    if (hz)
-        hipLaunchKernelGGL((pf_gemm_kernel<false, true>), dim3(P.max_tiles, P.hidden / 256),
-                           dim3(PF_THREADS), 0, s, P);
-    else
-        hipLaunchKernelGGL((pf_gemm_kernel<false, false>), dim3(P.max_tiles, P.hidden / 256),
-                           dim3(PF_THREADS), 0, s, P);
+    if (hz) pf_launch<false, true>(P, gx, s);
+    else pf_launch<false, false>(P, gx, s);
     ev_after(EV_PF_DOWN, s);
-    const size_t n_out = (size_t)n_tokens * P.hidden;
+    const size_t n_out = (size_t)n_tokens * (P.hidden / 8);
     hipLaunchKernelGGL(pf_combine_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, s,
                        P);
     return hipGetLastError();

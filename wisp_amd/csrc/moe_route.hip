@@ -242,9 +242,14 @@ __global__ void expert_offsets_kernel(const int* __restrict__ topk_idx, int n_pa
     for (int i = t; i < T * n_experts; i += T) cnt[i] = 0;
     __syncthreads();
     uint16_t* mine = cnt + (size_t)t * n_experts;
-    for (int p = p0; p < p1; p++) {
-        int e = topk_idx[p];
-        if (e >= 0 && e < n_experts) mine[e]++;
+    /* the chunk's ids are loaded 8 at a time: one memory round trip per 8 */
+    for (int p = p0; p < p1; p += 8) {
+        int ev[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) ev[q] = p + q < p1 ? topk_idx[p + q] : -1;
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            if (ev[q] >= 0 && ev[q] < n_experts) mine[ev[q]]++;
     }
     __syncthreads();
     /* per-expert exclusive prefix over chunks; totals */
@@ -265,14 +270,21 @@ __global__ void expert_offsets_kernel(const int* __restrict__ topk_idx, int n_pa
     }
     __syncthreads();
     for (int e = t; e <= n_experts; e += T) offsets[e] = s_off[e];
-    for (int p = p0; p < p1; p++) {
-        int e = topk_idx[p];
-        if (e >= 0 && e < n_experts) {
-            int pos = s_off[e] + mine[e]++;
-            order[pos] = p;
-            inv[p] = pos;
-        } else {
-            inv[p] = -1;
+    for (int p = p0; p < p1; p += 8) {
+        int ev[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) ev[q] = p + q < p1 ? topk_idx[p + q] : -1;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            if (p + q >= p1) break;
+            const int e = ev[q];
+            if (e >= 0 && e < n_experts) {
+                const int pos = s_off[e] + mine[e]++;
+                order[pos] = p + q;
+                inv[p + q] = pos;
+            } else {
+                inv[p + q] = -1;
+            }
         }
     }
 }
@@ -284,11 +296,14 @@ extern "C" hipError_t wisp_gpu_expert_offsets(const int* d_topk_idx, int n_token
         return hipErrorInvalidValue;
     long n_pairs = (long)n_tokens * top_k;
     /* chunks of at most 65535 pairs per thread (u16 counters) and a count
-     * table of at most 64 KiB of LDS */
+     * table of at most 128 KiB of LDS (gfx950 has 160 KiB per workgroup) */
     int T = 256;
-    while (T > 32 && (size_t)T * n_experts * 2 > 65536) T >>= 1;
+    while (T > 32 && (size_t)T * n_experts * 2 > 131072) T >>= 1;
     if ((n_pairs + T - 1) / T > 65535) return hipErrorInvalidValue;
     size_t lds = (size_t)T * n_experts * sizeof(uint16_t);
+    if (lds > 65536)
+        (void)hipFuncSetAttribute((const void*)expert_offsets_kernel,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     hipLaunchKernelGGL(expert_offsets_kernel, dim3(1), dim3(T), lds, s, d_topk_idx,
                        (int)n_pairs, n_experts, d_counts, d_offsets, d_order, d_inv);
     return hipGetLastError();
