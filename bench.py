@@ -330,6 +330,92 @@ def measure_prefill(layer, n_tokens, steps, warmup, seed=2048):
     }
 
 
+def measure_streaming(n_layers=8, steps=256, slot_frac=0.30, seed=55, n_templates=16):
+    """Expert-streaming decode: n_layers DeepSeek-V3-shape MoE layers whose
+    256 routed experts each live in pinned host RAM, a VRAM LRU of slot_frac
+    of all experts (the tier of include/wisp_amd.h section 6), one token per
+    step with Zipf(1.1) top-8 routing per layer, the shared expert resident.
+    The compute stream is synchronised after every layer, as a real decode
+    must (the next layer's routing needs this layer's output). Reports
+    us/token over all steps and over the second half (warm), the VRAM hit
+    rate (vram_hits / lookups) and the H2D rate, plus the rate of a plain
+    run of blob copies for comparison."""
+    from wisp_amd import moe, synth, tier
+    from wisp_amd.hip import DeviceBuffer, Event, PinnedBuffer, Stream, synchronize, to_device
+    s = synth.DSV3
+    E, k = s.n_experts, s.top_k
+    size = synth.blob_size(s.inter, s.hidden, s.group_size)
+    t0 = time.time()
+    rng = np.random.default_rng(seed)
+    temps = [synth.make_blob(np.random.default_rng([seed, i]), s.inter, s.hidden, s.group_size,
+                             expert=i) for i in range(n_templates)]
+    layers = []
+    for l in range(n_layers):
+        pb = PinnedBuffer(E * size)
+        for e in range(E):
+            pb.array[e * size:(e + 1) * size] = temps[(l * E + e) % n_templates]
+        layers.append(pb)
+    log(f"streaming: {n_layers} x {E} experts ({n_layers * E * size / 1e9:.1f} GB) pinned in "
+        f"{time.time() - t0:.1f}s")
+    ptrs = [layers[l].ptr + e * size for l in range(n_layers) for e in range(E)]
+    layout = moe.layout_from_blob(temps[0], has_zeros=False)
+    n_slots = int(round(slot_frac * n_layers * E))
+    t = tier.ExpertTier(n_layers, E, size, ptrs, n_slots, scratch_slots=k + 2)
+    shared = []
+    for l in range(n_layers):
+        d = DeviceBuffer(size + 16)
+        d.upload(temps[(l + 7) % n_templates], offset=8)
+        shared.append(d)
+    st = Stream()
+    ws = DeviceBuffer(moe.decode_workspace_bytes(layout, 1, k, True))
+    out32 = DeviceBuffer(4 * s.hidden)
+    xs = to_device(synth.make_x(rng, 16, s.hidden))
+    routes = [[synth.zipf_topk(rng, 1, E, k) for _ in range(n_layers)] for _ in range(steps)]
+    weights = [[synth.route_weights(rng, 1, k) for _ in range(n_layers)] for _ in range(steps)]
+    per_step = []
+    half = None
+    for step in range(steps):
+        if step == steps // 2:
+            half = t.stats()
+        c0 = time.perf_counter()
+        for l in range(n_layers):
+            t.moe_decode_layer(l, shared[l].ptr + 8, layout, xs.ptr + (step % 16) * s.hidden * 2, 1,
+                               routes[step][l], weights[step][l], ws, out32.ptr, 0, st.handle)
+            st.synchronize()
+        per_step.append(time.perf_counter() - c0)
+    end = t.stats()
+    wall = float(np.sum(per_step))
+    warm = float(np.sum(per_step[steps // 2:]))
+    # plain H2D rate of blob copies, same pinned source, no kernels
+    dst = DeviceBuffer(size * 4)
+    e0, e1 = Event(), Event()
+    from wisp_amd.hip import runtime, check, hipMemcpyHostToDevice
+    rt = runtime()
+    e0.record(st.handle)
+    n_copy = 24
+    for i in range(n_copy):
+        check(rt.hipMemcpyAsync(dst.ptr + (i % 4) * size, ptrs[(i * 37) % len(ptrs)], size,
+                                hipMemcpyHostToDevice, st.handle), "H2D")
+    e1.record(st.handle)
+    synchronize()
+    copy_gbs = n_copy * size / (e0.elapsed_ms(e1) * 1e-3) / 1e9
+    wh = {key: end[key] - half[key] for key in end}
+    res = {
+        "us_per_token": round(1e6 * wall / steps, 1),
+        "us_per_token_warm": round(1e6 * warm / (steps - steps // 2), 1),
+        "vram_hit_rate": round(end["vram_hits"] / end["lookups"], 4),
+        "vram_hit_rate_warm": round(wh["vram_hits"] / wh["lookups"], 4),
+        "h2d_gb": round(end["h2d_bytes"] / 1e9, 2),
+        "h2d_gbs_during_run": round(end["h2d_bytes"] / wall / 1e9, 2),
+        "h2d_gbs_plain_copies": round(copy_gbs, 2),
+        "stats": end, "layers": n_layers, "steps": steps, "vram_slots": n_slots,
+        "experts_total": n_layers * E, "blob_bytes": size,
+    }
+    t.close()
+    del layers
+    return res
+
+
 def copy_calibration(mib):
     """Five launches of a plain copy of `mib` MiB (source and destination
     both far larger than the Infinity Cache for mib >= 512)."""
@@ -359,6 +445,9 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline workload only")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the DeepSeek-V3 prefill grouped GEMM (2048 tokens)")
+    ap.add_argument("--streaming-only", action="store_true",
+                    help="only the 8-layer expert-streaming decode (VRAM tier)")
+    ap.add_argument("--stream-steps", type=int, default=256)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB 5 times (byte-counter calibration)")
     args = ap.parse_args()
@@ -374,6 +463,11 @@ def main():
         sys.exit(1)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+
+    if args.streaming_only:
+        r = measure_streaming(steps=args.stream_steps)
+        print(json.dumps({"deepseek-v3-streaming-8layers": r}), flush=True)
         return
 
     if args.prefill_only:
@@ -434,6 +528,9 @@ def main():
             log(f"{key}: {extra[key]}")
         extra["deepseek-v3-prefill-2048"] = measure_prefill(ds, 2048, 5, 2)
         log(f"deepseek-v3 prefill: {extra['deepseek-v3-prefill-2048']}")
+        del ds
+        extra["deepseek-v3-streaming-8layers"] = measure_streaming(steps=args.stream_steps)
+        log(f"streaming: {extra['deepseek-v3-streaming-8layers']}")
         result["extra"] = extra
     print(json.dumps(result), flush=True)
 

@@ -291,6 +291,113 @@ hipError_t wisp_gpu_moe_prefill_int4(const void* const* d_expert_table,
                                      hipStream_t s);
 
 /* ======================================================================= *
+ * 6. VRAM tier of the expert cache
+ *
+ *    Every expert blob of every layer sits in pinned host memory (the RAM
+ *    tier); a fixed number of VRAM slots caches the hot ones with the
+ *    reference's policy (csrc/core/wisp_engine.c:1138-1296): a first touch
+ *    takes a free slot or rides the scratch ring; a later RAM hit is served
+ *    through the scratch ring until the expert has been hit promote_hits
+ *    times (the reference's WISP_PROMOTE_HITS = 3), then it is promoted
+ *    into a slot, evicting the least recently used resident expert that
+ *    the current layer has not resolved. Copies are hipMemcpyAsync on the
+ *    tier's own stream, ordered by events. One owner thread; not
+ *    thread-safe.
+ * ======================================================================= */
+
+/* Lookup paths (same numbering as the reference trace harness). */
+enum {
+    WISP_TIER_VRAM_HIT = 0,       /* resident in a VRAM slot                   */
+    WISP_TIER_RAM_SCRATCH = 1,    /* RAM hit below the promotion count          */
+    WISP_TIER_RAM_PROMOTE = 2,    /* RAM hit that earned a VRAM slot            */
+    WISP_TIER_COLD_VRAM = 3,      /* first touch, free slot available           */
+    WISP_TIER_COLD_SCRATCH = 4    /* first touch, no free slot                  */
+};
+/* Indices of the statistics array. The VRAM hit rate is
+ * VRAM_HITS / LOOKUPS; the reference reports (vram + ram) / total
+ * (csrc/core/wisp_engine.c:2343-2344), which is always 1 here. */
+enum {
+    WISP_TIER_LOOKUPS = 0, WISP_TIER_VRAM_HITS, WISP_TIER_RAM_HITS, WISP_TIER_FIRST_TOUCH,
+    WISP_TIER_PROMOTIONS, WISP_TIER_EVICTIONS, WISP_TIER_SCRATCH_SERVES, WISP_TIER_H2D_BYTES,
+    WISP_TIER_N_STATS
+};
+
+/* The policy alone, on the host (no device calls): for tests and for
+ * engines that move the bytes themselves. */
+typedef struct WispTierPolicy WispTierPolicy;
+WispTierPolicy* wisp_tier_policy_create(int n_layers, int n_experts,
+                                        int n_slots, int scratch_slots,
+                                        int promote_hits);
+void wisp_tier_policy_destroy(WispTierPolicy* t);
+/* Starts the lookups of one layer: experts resolved from here on are not
+ * evicted until the next call. */
+void wisp_tier_policy_begin_layer(WispTierPolicy* t);
+/* One lookup; returns the path (WISP_TIER_*), or -1 for bad arguments.
+ * *slot = VRAM slot or scratch-ring index; *victim_layer / *victim_expert =
+ * the expert evicted by a promotion, else -1. */
+int wisp_tier_policy_lookup(WispTierPolicy* t, int layer, int expert,
+                            int* slot, int* victim_layer, int* victim_expert);
+/* out[WISP_TIER_N_STATS] (H2D_BYTES stays 0). */
+void wisp_tier_policy_stats(const WispTierPolicy* t, uint64_t* out);
+
+/* The tier with its device memory. host_blobs: [n_layers * n_experts]
+ * pinned host pointers (hipHostMalloc), blob of expert e of layer l at
+ * index l * n_experts + e, each blob_bytes long. Allocates n_slots +
+ * scratch_slots device slots (blob at slot + 8, so that every section is
+ * 16-byte aligned) and a device table [n_layers][n_experts] of blob
+ * pointers. Returns NULL and sets *err on failure. */
+typedef struct WispExpertTier WispExpertTier;
+WispExpertTier* wisp_tier_create(int n_layers, int n_experts,
+                                 size_t blob_bytes,
+                                 const void* const* host_blobs, int n_slots,
+                                 int scratch_slots, int promote_hits,
+                                 hipError_t* err);
+void wisp_tier_destroy(WispExpertTier* t);
+/* Device table row of a layer: [n_experts] blob pointers, valid for the
+ * experts of the last wisp_tier_fetch_layer of that layer. */
+void** wisp_tier_device_table(WispExpertTier* t, int layer);
+/* Resolves n expert ids of one layer (host array; ids < 0 are skipped):
+ * policy lookups, hipMemcpyAsync from the pinned blobs on the tier's
+ * stream for everything not already resident (each copy first waits for
+ * the kernels that last read its slot), then the layer's table row is
+ * copied to the device on `compute`. out_path[i] (may be NULL) receives
+ * each id's path. Kernels reading experts whose path is not
+ * WISP_TIER_VRAM_HIT must be launched after wisp_tier_wait_copies; VRAM
+ * hits can be used at once. The distinct valid ids must not outnumber
+ * the scratch slots (hipErrorInvalidValue), so that the ring never wraps
+ * within a layer (the reference sizes it top_k + 2 for one token).
+ * Replaces the per-expert wisp_expert_fetch calls of run_moe
+ * (csrc/core/wisp_engine.c:1653-1665). */
+hipError_t wisp_tier_fetch_layer(WispExpertTier* t, int layer,
+                                 const int* expert_ids, int n, int* out_path,
+                                 hipStream_t compute);
+/* Makes `compute` wait for the copies of the last fetch. */
+hipError_t wisp_tier_wait_copies(WispExpertTier* t, hipStream_t compute);
+/* Call after the last launch that reads the layer's experts on `compute`:
+ * a later copy into one of their slots waits for it. */
+hipError_t wisp_tier_release_layer(WispExpertTier* t, hipStream_t compute);
+/* out[WISP_TIER_N_STATS]. */
+void wisp_tier_stats(const WispExpertTier* t, uint64_t* out);
+
+/* One MoE decode layer (n_tokens * top_k <= 256) whose routing is known on
+ * the host (h_topk_idx / h_topk_w [n_tokens][top_k], as run_moe has it
+ * after its routing sync, csrc/core/wisp_engine.c:1576): fetch, then the
+ * fused decode of the experts already resident plus the shared expert on
+ * `compute` while the missing ones are copied on the tier's stream, then
+ * the copied experts as an accumulating second pass, then release. The
+ * fp32 output d_out_f32 is required (the second pass accumulates into
+ * it); d_out_f16 may be NULL. Workspace as wisp_gpu_moe_decode_int4. */
+hipError_t wisp_tier_moe_decode_layer(WispExpertTier* t, int layer,
+                                      const void* d_shared_blob,
+                                      const WispExpertLayout* L,
+                                      const void* d_x, int x_dtype,
+                                      int n_tokens, const int* h_topk_idx,
+                                      const float* h_topk_w, int top_k,
+                                      void* d_workspace, size_t workspace_bytes,
+                                      float* d_out_f32, wisp_half* d_out_f16,
+                                      hipStream_t compute);
+
+/* ======================================================================= *
  * 9. Profiling hook
  * ======================================================================= */
 
