@@ -448,6 +448,8 @@ def main():
     ap.add_argument("--streaming-only", action="store_true",
                     help="only the 8-layer expert-streaming decode (VRAM tier)")
     ap.add_argument("--stream-steps", type=int, default=256)
+    ap.add_argument("--dsv3-decode-only", type=int, default=0, metavar="M",
+                    help="only the DeepSeek-V3 decode layer with M tokens (profiling runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB 5 times (byte-counter calibration)")
     args = ap.parse_args()
@@ -463,6 +465,12 @@ def main():
         sys.exit(1)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+
+    if args.dsv3_decode_only:
+        ds = Layer(synth.DSV3, args.dsv3_decode_only, seed=777, n_sets=1)
+        r = measure(ds, args.steps, args.warmup)
+        print(json.dumps({f"deepseek-v3-decode-m{args.dsv3_decode_only}": r}), flush=True)
         return
 
     if args.streaming_only:

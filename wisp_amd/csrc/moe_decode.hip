@@ -27,8 +27,8 @@
  *             reduced through LDS in a fixed order; the epilogue writes
  *             h' = w_route * silu(g) * u in fp16, already permuted for the
  *             down kernel.
- *   down    : grid (hidden/16 row tiles) x (unique experts x K chunks of
- *             4096). Each workgroup writes its partial sums (routing weights
+ *   down    : grid (hidden/16 row tiles) x (unique experts x K chunks of at
+ *             most 4096). Each workgroup writes its partial sums (routing weights
  *             are already folded into h').
  *   combine : adds the partials in a fixed order (shared expert, then
  *             routed experts in unique-list order, then K chunk), so the
@@ -44,7 +44,7 @@
 #define DEC_MAX_TOKENS 4
 #define DEC_MAX_TOPK 64
 #define DEC_MAX_WAVES 8
-#define DEC_CHUNK_BLOCKS 32   /* down-projection K chunk per workgroup: 4096 elements */
+#define DEC_CHUNK_MAX 32      /* down-projection K chunk per workgroup: at most 32 blocks of 128 */
 #define DEC_ROUTE_FUSE_BYTES (256 * 1024)   /* router matrices up to this size run in prep */
 #define DEC_ROUTE_MAX_EXPERTS 1024
 #define DEC_PREP_THREADS 512
@@ -53,7 +53,8 @@ struct DecodeParams {
     uint64_t p_off[3], s_off[3], z_off[3];
     int hidden, inter, gs, has_zeros;
     int gshift;           /* log2(gs * NG / 128): block -> group index */
-    int n_chunks;         /* down-projection K chunks: ceil(inter/128 / DEC_CHUNK_BLOCKS) */
+    int n_chunks;         /* down-projection K chunks of chunk_blocks 128-wide blocks */
+    int chunk_blocks;     /* a multiple of 8 (one wave per 8 blocks), see dec_chunk_blocks */
     uint32_t m_lo, m_hi, one024;  /* unpack masks 0x000F000F, 0x00F000F0, 0x64006400 */
     int max_u;
     int M;
@@ -88,6 +89,14 @@ struct RouteArgs {
 
 __host__ __device__ constexpr int align_up_dev(int v, int a) { return (v + a - 1) / a * a; }
 
+/* Dynamic LDS of the prep kernel in routing modes 1 and 2: 64-bit selection
+ * keys, M rows of scores, and (mode 2) the M token rows. */
+static inline size_t prep_lds_bytes(int mode, int n_experts, int M, int hidden, size_t xsz) {
+    if (mode == 0) return 0;
+    return (size_t)align_up_dev(n_experts * 8, 16) + align_up_dev(M * n_experts * 4, 16) +
+           (mode == 2 ? (size_t)M * hidden * xsz : 0);
+}
+
 /* One workgroup of DEC_PREP_THREADS. Every global load it needs (the expert
  * table, and in mode 2 each wave's first router row and the token rows) is
  * issued before the first barrier, so the kernel costs about one memory
@@ -101,6 +110,7 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     __shared__ float s_w[DEC_MAX_TOKENS * DEC_MAX_TOPK];
     __shared__ int s_wcount[NWV];
     __shared__ const uint8_t* s_tab[DEC_ROUTE_MAX_EXPERTS];
+    __shared__ float s_red[32];
     const int M = P.M;
     const int n_pairs = M * top_k;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -113,13 +123,19 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     }
 
     if (R.mode != 0) {
-        /* dynamic LDS: selection keys [M][n_experts], scores [M][n_experts]
-         * (the raw logits first, in mode 2), then x [M][hidden] (mode 2) */
+        /* dynamic LDS: 64-bit selection keys [n_experts] (scratch of the
+         * top-k), scores [M][n_experts] (the raw logits first), then x
+         * [M][hidden] (mode 2) */
         extern __shared__ __attribute__((aligned(16))) uint8_t lds_raw[];
-        float* s_key = (float*)lds_raw;
-        float* s_sc = s_key + M * n_experts;
-        if (R.mode == 2) {
-            XT* s_x = (XT*)(lds_raw + align_up_dev(2 * M * n_experts * 4, 16));
+        uint64_t* s_ck = (uint64_t*)lds_raw;
+        float* s_sc = (float*)(lds_raw + align_up_dev(n_experts * 8, 16));
+        if (R.mode == 1) {
+            /* raw logits from router_logits_kernel, loaded with everything else */
+            for (int i = threadIdx.x; i < M * n_experts; i += blockDim.x) s_sc[i] = R.logits[i];
+            __syncthreads();
+        } else {
+            XT* s_x = (XT*)(lds_raw + align_up_dev(n_experts * 8, 16) +
+                            align_up_dev(M * n_experts * 4, 16));
             u4 wrow[ROUTE_UNROLL];
             if (wv < n_experts) router_row_load(R.W + (size_t)wv * P.hidden, P.hidden, lane, wrow);
             stage_rows<XT>(s_x, x, M, P.hidden);
@@ -132,12 +148,10 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
             }
             __syncthreads();
         }
-        if (wv < M) {
-            const float* lg = R.mode == 2 ? s_sc + wv * n_experts : R.logits + (size_t)wv * n_experts;
-            topk_lds(lg, R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr, s_key + wv * n_experts,
-                     s_sc + wv * n_experts, R.logits + (size_t)wv * n_experts, n_experts, top_k,
-                     R.kind, s_e + wv * top_k, s_w + wv * top_k, lane);
-        }
+        for (int t = 0; t < M; t++)
+            topk_block(s_sc + t * n_experts, R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr, s_ck,
+                       s_sc + t * n_experts, s_red, R.logits + (size_t)t * n_experts, n_experts,
+                       top_k, R.kind, s_e + t * top_k, s_w + t * top_k);
     } else {
         for (int p = threadIdx.x; p < n_pairs; p += blockDim.x) {
             s_e[p] = R.idx[p];
@@ -542,7 +556,7 @@ __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void gateup_kernel(const Decode
 /* ======================================================================= */
 
 /* grid (hidden / (16 TILES), max_u * n_chunks): workgroup (row tile,
- * unique expert u, K chunk c of DEC_CHUNK_BLOCKS blocks) writes
+ * unique expert u, K chunk c of chunk_blocks blocks) writes
  * part[u][c][v][row] = down_u[row, chunk] . h'_u[v][chunk] (routing weight
  * already folded into h'). */
 template <int M, int NG, int TILES, int NB, bool HZ>
@@ -560,12 +574,12 @@ __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void down_kernel(const DecodePa
     const int col = lane & 15, j = lane >> 4;
     const int nblk = K >> 7;
     const int G = K / P.gs;
-    const int cb0 = c * DEC_CHUNK_BLOCKS, cb1 = min(cb0 + DEC_CHUNK_BLOCKS, nblk);
+    const int cb0 = c * P.chunk_blocks, cb1 = min(cb0 + P.chunk_blocks, nblk);
     const int g_lo = (cb0 * NG) >> P.gshift, g_hi = (((cb1 * NG) - 1) >> P.gshift) + 1;
     const int nb = cb1 - cb0;
     /* wave w owns blocks [cb0 + NB w, cb0 + NB w + NB) of the chunk */
     const int b0 = cb0 + wave * NB, b1 = min(b0 + NB, cb1);
-    const LdsMap L = lds_map(M, NT, DEC_CHUNK_BLOCKS * 128, g_hi - g_lo, HZ, nw);
+    const LdsMap L = lds_map(M, NT, P.chunk_blocks * 128, g_hi - g_lo, HZ, nw);
 
     const uint8_t* wp[NT];
 #pragma unroll
@@ -693,6 +707,16 @@ extern "C" hipError_t wisp_expert_layout_check(const WispExpertLayout* L) {
     return hipSuccess;
 }
 
+/* Down-projection K chunk: the fewest chunks of at most DEC_CHUNK_MAX
+ * blocks, as even as a multiple of 8 blocks (one wave each) allows
+ * (Mixtral inter 14336: 32, 32, 32, 16 blocks; measured faster on MI355X
+ * than 2 chunks of 56 blocks at 7 waves). */
+static int dec_chunk_blocks(int nblk) {
+    const int nch = (nblk + DEC_CHUNK_MAX - 1) / DEC_CHUNK_MAX;
+    const int c = (nblk + nch - 1) / nch;
+    return (c + 7) / 8 * 8;
+}
+
 struct WsLayout {
     size_t nu, ublob, uw, xconv, hperm, part, total;
     int max_u;
@@ -707,7 +731,8 @@ static WsLayout ws_layout(const WispExpertLayout* L, int M, int top_k, int has_s
     w.uw = off; off = align_up(off + (size_t)w.max_u * 4 * sizeof(float), 256);
     w.xconv = off; off = align_up(off + (size_t)M * L->cols[0] * 2, 256);
     w.hperm = off; off = align_up(off + (size_t)w.max_u * M * L->rows[0] * 2, 256);
-    const size_t nch = ((L->rows[0] / 128) + DEC_CHUNK_BLOCKS - 1) / DEC_CHUNK_BLOCKS;
+    const int nblk = (int)(L->rows[0] / 128);
+    const size_t nch = (nblk + dec_chunk_blocks(nblk) - 1) / dec_chunk_blocks(nblk);
     w.part = off; off = align_up(off + (size_t)w.max_u * nch * M * L->cols[0] * 4, 256);
     w.total = off;
     return w;
@@ -736,11 +761,12 @@ static void launch_gateup(const DecodeParams& P, hipStream_t s) {
 
 template <int M, int NG, int TILES, int NB, bool HZ>
 static void launch_down(const DecodeParams& P, hipStream_t s) {
-    const int chunk = (P.inter / 128) < DEC_CHUNK_BLOCKS ? (P.inter / 128) : DEC_CHUNK_BLOCKS;
+    const int nblk = P.inter / 128;
+    const int chunk = nblk < P.chunk_blocks ? nblk : P.chunk_blocks;
     const int waves = (chunk + NB - 1) / NB;
-    /* LDS sized for the largest chunk: full DEC_CHUNK_BLOCKS and its groups */
-    const int ng_hi = (((DEC_CHUNK_BLOCKS * NG) - 1) >> P.gshift) + 2;
-    const LdsMap L = lds_map(M, TILES, DEC_CHUNK_BLOCKS * 128, ng_hi, HZ, waves);
+    /* LDS sized for the largest chunk and its groups */
+    const int ng_hi = (((P.chunk_blocks * NG) - 1) >> P.gshift) + 2;
+    const LdsMap L = lds_map(M, TILES, P.chunk_blocks * 128, ng_hi, HZ, waves);
     auto k = down_kernel<M, NG, TILES, NB, HZ>;
     if (L.bytes > 65536)
         (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, L.bytes);
@@ -803,7 +829,8 @@ static hipError_t decode_run(const void* const* d_expert_table, const void* d_sh
         while ((128 << sh) < ngs) sh++;
         P.gshift = sh;
     }
-    P.n_chunks = ((P.inter / 128) + DEC_CHUNK_BLOCKS - 1) / DEC_CHUNK_BLOCKS;
+    P.chunk_blocks = dec_chunk_blocks(P.inter / 128);
+    P.n_chunks = (P.inter / 128 + P.chunk_blocks - 1) / P.chunk_blocks;
     P.m_lo = 0x000F000Fu;
     P.m_hi = 0x00F000F0u;
     P.one024 = 0x64006400u;
@@ -823,9 +850,7 @@ static hipError_t decode_run(const void* const* d_expert_table, const void* d_sh
     P.accumulate = accumulate ? 1 : 0;
 
     const size_t xsz = x_dtype == WISP_DTYPE_F16 ? 2 : 4;
-    const size_t lds = R.mode == 0 ? 0
-                       : align_up_dev(2 * M * n_experts * 4, 16) +
-                             (R.mode == 2 ? M * P.hidden * xsz : 0);
+    const size_t lds = prep_lds_bytes(R.mode, n_experts, M, P.hidden, xsz);
     ev_before(EV_PREP, s);
     if (x_dtype == WISP_DTYPE_F16)
         hipLaunchKernelGGL(decode_prep_kernel<uint16_t>, dim3(1), dim3(DEC_PREP_THREADS), lds, s, P, R,
@@ -892,7 +917,7 @@ extern "C" hipError_t wisp_gpu_moe_layer_decode_int4(
     if (wisp_expert_layout_check(L) != hipSuccess) return hipErrorInvalidValue;
     const int hidden = (int)L->cols[0];
     const size_t xsz = x_dtype == WISP_DTYPE_F16 ? 2 : 4;
-    const size_t prep_lds = align_up_dev(2 * n_tokens * n_experts * 4, 16) + n_tokens * hidden * xsz;
+    const size_t prep_lds = prep_lds_bytes(2, n_experts, n_tokens, hidden, xsz);
     const bool fuse = (size_t)n_experts * hidden * 2 <= DEC_ROUTE_FUSE_BYTES &&
                       hidden <= ROUTE_UNROLL * WAVE * 8 &&
                       prep_lds <= 65536 && (uintptr_t)d_router_w % 16 == 0 &&

@@ -120,26 +120,33 @@ hipError_t wisp_amd__router_logits(const wisp_half* W, const wisp_half* bias, co
 /* ======================================================================= */
 
 /* scores_out[t, e] = softmax probability or sigmoid score; idx/w [t, k].
- * One wave per token; dynamic LDS of 2 * n_experts floats. */
-__global__ __launch_bounds__(64) void topk_kernel(const float* logits,
-                                                  const uint16_t* __restrict__ bias,
-                                                  float* scores_out,
-                                                  int n_tokens, int n_experts, int top_k,
-                                                  int kind, int* __restrict__ out_idx,
-                                                  float* __restrict__ out_w) {
-    extern __shared__ float topk_lds_buf[];
+ * One workgroup of 256 per token; dynamic LDS of topk_lds_bytes. */
+static inline size_t topk_lds_bytes(int n_experts) {
+    return (size_t)((n_experts + 1) & ~1) * 8 + (size_t)n_experts * 4;
+}
+
+__global__ __launch_bounds__(256) void topk_kernel(const float* logits,
+                                                   const uint16_t* __restrict__ bias,
+                                                   float* scores_out,
+                                                   int n_tokens, int n_experts, int top_k,
+                                                   int kind, int* __restrict__ out_idx,
+                                                   float* __restrict__ out_w) {
+    extern __shared__ __attribute__((aligned(16))) uint64_t topk_buf[];
+    __shared__ float s_red[32];
     const int t = blockIdx.x;
     if (t >= n_tokens) return;
-    topk_lds(logits + (size_t)t * n_experts, bias, topk_lds_buf, topk_lds_buf + n_experts,
-             scores_out + (size_t)t * n_experts, n_experts, top_k, kind,
-             out_idx + (size_t)t * top_k, out_w + (size_t)t * top_k, threadIdx.x);
+    uint64_t* s_ck = topk_buf;
+    float* s_sc = (float*)(topk_buf + ((n_experts + 1) & ~1));
+    topk_block(logits + (size_t)t * n_experts, bias, s_ck, s_sc, s_red,
+               scores_out + (size_t)t * n_experts, n_experts, top_k, kind,
+               out_idx + (size_t)t * top_k, out_w + (size_t)t * top_k);
 }
 
 static hipError_t launch_topk(const float* d_logits, const uint16_t* d_bias, float* d_scores,
                               int n_tokens, int n_experts, int top_k, int kind,
                               int* d_idx, float* d_w, hipStream_t s) {
-    hipLaunchKernelGGL(topk_kernel, dim3(n_tokens), dim3(64),
-                       (size_t)2 * n_experts * sizeof(float), s, d_logits, d_bias,
+    hipLaunchKernelGGL(topk_kernel, dim3(n_tokens), dim3(256), topk_lds_bytes(n_experts), s,
+                       d_logits, d_bias,
                        d_scores, n_tokens, n_experts, top_k, kind, d_idx, d_w);
     return hipGetLastError();
 }

@@ -1,5 +1,5 @@
 /*
- * route_common.h — router dot products and the wave-level top-k selection
+ * route_common.h — router dot products and the workgroup top-k selection
  * shared by the routing kernels and the fused decode prep (internal).
  *
  * Selection rule (csrc/core/wisp_engine.c:803-815, csrc/cuda/router.cu:
@@ -125,72 +125,113 @@ __device__ __forceinline__ void stage_rows(XT* dst, const XT* __restrict__ src, 
     for (int i = threadIdx.x; i < n; i += blockDim.x) ((u4*)dst)[i] = ((const u4*)src)[i];
 }
 
-/* a beats b: larger key, or equal key and lower index. NaN never wins. */
-__device__ __forceinline__ bool route_beats(float av, int ai, float bv, int bi) {
-    return av > bv || (av == bv && ai >= 0 && (bi < 0 || ai < bi));
+/* Selection key of expert e as one unsigned 64-bit number: the high word
+ * maps the float key to an unsigned integer of the same order (-0 as +0,
+ * NaN to 0 below every number), the low word is ~e, so "a beats b"
+ * (larger key, or equal key and lower index) is a single compare
+ * composite(a) > composite(b). */
+__device__ __forceinline__ uint64_t route_composite(float key, int e) {
+    uint32_t u = __float_as_uint(key == 0.0f ? 0.0f : key);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    if (key != key) u = 0u;
+    return ((uint64_t)u << 32) | (uint32_t)~(uint32_t)e;
 }
 
-/* One wave, one token. lg: the token's raw logits [n_experts] (global or
- * LDS; for SOFTMAX they already include the bias). s_key / s_sc: LDS
- * scratch of n_experts floats each; s_sc may alias lg (entry e is only
- * ever touched by lane e % 64). Writes the post-activation scores to
- * scores_out, and idx/w [top_k] (written by lane 0). For SIGMOID the bias
- * (if any) is added to the score for selection only; weights are the
- * selected unbiased scores renormalised to sum 1. Loops are runtime loops:
- * this runs once per token and its code size is what costs time. */
-__device__ __noinline__ void topk_lds(const float* lg, const uint16_t* __restrict__ bias,
-                                      float* s_key, float* s_sc, float* scores_out,
-                                      int n_experts, int top_k, int kind, int* out_idx,
-                                      float* out_w, int lane) {
+typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+
+/* All threads of the workgroup, one token. lg: the token's raw logits
+ * [n_experts] (LDS or global; for SOFTMAX they already include the bias).
+ * s_ck: LDS scratch of n_experts uint64, 16-byte aligned; s_sc: LDS
+ * scratch of n_experts floats (it may alias lg when lg is in LDS: every
+ * entry is read by its own thread before it is written); s_red: LDS
+ * scratch of 32 floats. Writes the post-activation scores to scores_out
+ * and the selection to out_idx/out_w [top_k] (LDS or global). For SIGMOID
+ * the bias (if any) is added to the score for selection only; weights are
+ * the selected unbiased scores renormalised to sum 1.
+ *
+ * Selection by rank, not by k passes of an argmax: expert e's rank is the
+ * number of experts whose composite key exceeds its own; ranks below top_k
+ * are the selection in order, which is what k passes of "largest untaken,
+ * ties to the lowest index" produce. Each expert is ranked by two half
+ * waves (lanes l and l+32), each counting half the keys with branch-free
+ * 64-bit compares on 16-byte broadcast LDS reads, then summed with one
+ * cross-half shuffle. NaN keys are never selected; with fewer than top_k
+ * candidates the rest are -1 with weight 0. */
+__device__ __forceinline__ void topk_block(const float* lg, const uint16_t* __restrict__ bias,
+                                           uint64_t* s_ck, float* s_sc, float* s_red,
+                                           float* scores_out, int n_experts, int top_k,
+                                           int kind, int* out_idx, float* out_w) {
     const bool sig = kind == WISP_ROUTER_SIGMOID;
+    const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wv = tid >> 6;
+    const int nw = (nt + 63) >> 6;
     float mx = -INFINITY;
-    for (int e = lane; e < n_experts; e += WAVE) {
+    for (int e = tid; e < n_experts; e += nt) {
         const float l = lg[e];
         float k = l;
         if (sig && bias) k = 1.0f / (1.0f + __expf(-l)) + half_bits_to_float(bias[e]);
-        s_key[e] = k;
+        s_ck[e] = route_composite(k, e);
         s_sc[e] = l;
         mx = fmaxf(mx, l);
     }
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, WAVE));
+    if (lane == 0) s_red[wv] = mx;
+    for (int q = tid; q < top_k; q += nt) {
+        out_idx[q] = -1;
+        out_w[q] = 0.0f;
+    }
+    __syncthreads();
+    mx = s_red[0];
+    for (int q = 1; q < nw; q++) mx = fmaxf(mx, s_red[q]);
     float denom = 0.0f;
-    for (int e = lane; e < n_experts; e += WAVE) {
+    for (int e = tid; e < n_experts; e += nt) {
         const float l = s_sc[e];
         const float v = sig ? 1.0f / (1.0f + __expf(-l)) : __expf(l - mx);
         s_sc[e] = v;
         denom += v;
     }
     denom = wave_sum(denom);
+    __syncthreads();   /* every thread has read s_red for the max */
+    if (lane == 0) s_red[wv] = denom;
+    __syncthreads();
+    denom = 0.0f;
+    for (int q = 0; q < nw; q++) denom += s_red[q];
     const float inv = 1.0f / (denom > 0.0f ? denom : 1.0f);
-    for (int e = lane; e < n_experts; e += WAVE) {
+    for (int e = tid; e < n_experts; e += nt) {
         float v = s_sc[e];
         if (!sig) v *= inv;
         s_sc[e] = v;
         scores_out[e] = v;
     }
-    float wsum = 0.0f;
-    for (int k = 0; k < top_k; k++) {
-        float bv = -INFINITY, bs = 0.0f;
-        int bi = -1;
-        for (int e = lane; e < n_experts; e += WAVE) {
-            const float kv = s_key[e];
-            if (route_beats(kv, e, bv, bi)) { bv = kv; bi = e; bs = s_sc[e]; }
+    /* ranks: half h of the wave counts key pairs [lo, hi) of its expert */
+    const int n_pairs = n_experts >> 1;
+    const int half_pairs = (n_pairs + 1) >> 1;
+    const int h = lane >> 5;
+    const int lo = h * half_pairs, hi = min(n_pairs, lo + half_pairs);
+    const u64x2* ck2 = (const u64x2*)s_ck;
+    for (int base = wv * 32; base < n_experts; base += nw * 32) {
+        const int e = base + (lane & 31);
+        const uint64_t ce = e < n_experts ? s_ck[e] : ~0ull;
+        int rank = 0;
+#pragma unroll 8
+        for (int q = lo; q < hi; q++) {
+            const u64x2 v = ck2[q];
+            rank += (v.x > ce) + (v.y > ce);
         }
-        for (int off = 32; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(bv, off, WAVE);
-            const int oi = __shfl_xor(bi, off, WAVE);
-            const float os = __shfl_xor(bs, off, WAVE);
-            if (route_beats(ov, oi, bv, bi)) { bv = ov; bi = oi; bs = os; }
-        }
-        if (bi >= 0 && (bi % WAVE) == lane) s_key[bi] = NAN;   /* taken: never wins again */
-        if (lane == 0) {
-            out_idx[k] = bi;
-            const float w = bi >= 0 ? bs : 0.0f;
-            out_w[k] = w;
-            wsum += w;
-        }
+        if (h == 1 && (n_experts & 1)) rank += s_ck[n_experts - 1] > ce;
+        rank += __shfl_xor(rank, 32, WAVE);
+        if (h == 0 && e < n_experts && (ce >> 32) != 0 && rank < top_k) out_idx[rank] = e;
     }
-    if (lane == 0 && wsum > 0.0f) {
-        for (int k = 0; k < top_k; k++) out_w[k] /= wsum;
+    __syncthreads();   /* selection and final scores visible */
+    if (tid == 0) {
+        float wsum = 0.0f;
+        for (int q = 0; q < top_k; q++) {
+            const int e = out_idx[q];
+            const float v = e >= 0 ? s_sc[e] : 0.0f;
+            out_w[q] = v;
+            wsum += v;
+        }
+        if (wsum > 0.0f)
+            for (int q = 0; q < top_k; q++) out_w[q] /= wsum;
     }
+    __syncthreads();
 }
