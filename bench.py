@@ -174,11 +174,12 @@ def time_layer(layer, steps, warmup):
     lib.wisp_amd_set_kernel_events(None, 0)
     synchronize()
     kern = {}
-    kinds = (("prep", EV_PREP), ("gate_up", EV_GATEUP), ("down", EV_DOWN), ("combine", EV_COMBINE))
+    kinds = (("prep", EV_PREP), ("gate_up", EV_GATEUP), ("down", EV_DOWN))
     if layer.separate_router():
         kinds = (("router_gemv", EV_ROUTE),) + kinds
     for name, k in kinds:
-        kern[name] = 1e3 * float(np.mean([evs[i][2 * k].elapsed_ms(evs[i][2 * k + 1]) for i in range(steps)]))
+        kern[name] = 1e3 * float(np.mean([evs[i][2 * k].elapsed_ms(evs[i][2 * k + 1])
+                                          for i in range(steps)]))
     return {"us_per_layer": 1e3 * dev_ms / steps, "eager_us_per_layer": 1e3 * eager_ms / steps,
             "host_us_per_layer": 1e3 * host_ms / steps, "kernel_us": kern}
 

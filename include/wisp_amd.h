@@ -405,8 +405,9 @@ hipError_t wisp_tier_moe_decode_layer(WispExpertTier* t, int layer,
  * events[2*k+1] after each kernel of kind k < n_pairs on the launch stream:
  * k = 0 router (wisp_gpu_moe_route, or the router GEMV launch of
  * wisp_gpu_moe_layer_decode_int4), 1 decode prep, 2 decode gate/up,
- * 3 decode down, 4 decode combine, 5 prefill gate/up, 6 prefill down. Process-wide; for
- * timing runs only; not thread-safe. */
+ * 3 decode down (it also writes the layer output), 4 unused, 5 prefill
+ * gate/up, 6 prefill down. Process-wide; for timing runs only; not
+ * thread-safe. */
 void wisp_amd_set_kernel_events(hipEvent_t* events, int n_pairs);
 
 /* Library version string. */

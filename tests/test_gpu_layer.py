@@ -19,10 +19,11 @@ pytestmark = pytest.mark.gpu
 
 
 def _keys(W, x, bias, kind):
-    """float64 selection keys of one token."""
+    """float64 selection keys of one token (a NaN key, never selected, as -inf)."""
     l = W.astype(np.float64) @ x.astype(np.float64)
     b = bias.astype(np.float64) if bias is not None else 0.0
-    return l + b if kind == "softmax" else 1.0 / (1.0 + np.exp(-l)) + b
+    k = l + b if kind == "softmax" else 1.0 / (1.0 + np.exp(-l)) + b
+    return np.where(np.isnan(k), -np.inf, k)
 
 
 def _near_tie(W, x, bias, kind, k):
@@ -30,14 +31,16 @@ def _near_tie(W, x, bias, kind, k):
     selection to be decided by fp32 summation order (the logits' fp32 error
     is ~1e-7 here; 2e-5 leaves a wide margin)."""
     key = _keys(W, x, bias, kind)
-    srt = np.sort(key)[::-1]
-    return np.min(np.abs(np.diff(srt[: k + 1]))) <= 2e-5 * max(np.max(np.abs(key)), 1.0)
+    srt = np.sort(key[np.isfinite(key)])[::-1]
+    return np.min(np.abs(np.diff(srt[: k + 1]))) <= 2e-5 * max(np.max(np.abs(srt)), 1.0)
 
 
 def run_layer(seed, inter, hidden, n_exp, top_k, M, kind, shared, use_bias, repeat=1,
-              gs=128, zeros=False):
+              gs=128, zeros=False, nan_rows=()):
     rng = np.random.default_rng(seed)
     W = synth.make_router(rng, n_exp, hidden, std=0.05)
+    for r in nan_rows:
+        W[r] = np.float16("nan")
     bias = (rng.standard_normal(n_exp) * 0.1).astype(np.float16) if use_bias else None
     x = synth.make_x(rng, M, hidden)
     # upload only the experts the routing can reach: each token's k + 4 best
@@ -83,6 +86,7 @@ def run_layer(seed, inter, hidden, n_exp, top_k, M, kind, shared, use_bias, repe
             assert set(oi.tolist()) <= set(cand)
             assert gi[t].tolist() == oi.tolist(), (t, gi[t], oi)
             assert np.allclose(gw[t], ow, rtol=1e-4, atol=1e-6), (t, gw[t], ow)
+        assert not set(gi[t].tolist()) & set(nan_rows), (t, gi[t])
         want = O.moe_combine(blobs, sh_blob, x[t].astype(np.float32), oi, ow)
         assert_close(g32[t], want, f"token {t} fp32")
         assert_close(g16[t], want, f"token {t} fp16")
@@ -110,6 +114,22 @@ def test_separate_router_launch(kind):
     # 256 experts x 1024 hidden x 2 B = 512 KiB router: logits in their own launch
     print(f"layer {kind} separate-router", flush=True)
     run_layer(700, 256, 1024, 256, 8, 3, kind, shared=True, use_bias=(kind == "sigmoid"))
+
+
+def test_one_token_64_experts_separate_router():
+    # 64 experts x 2304 hidden x 2 B = 288 KiB router: logits in their own
+    # launch, then the one-wave selection at its largest expert count
+    print("layer M=1 E=64 separate-router", flush=True)
+    run_layer(710, 256, 2304, 64, 8, 1, "softmax", shared=True, use_bias=True)
+
+
+@pytest.mark.parametrize("n_exp", [32, 256])
+def test_sigmoid_nan_logit_never_selected(n_exp):
+    # a NaN router row gives a NaN key: the oracle's "largest untaken" never
+    # picks it, and neither may the device (one-wave and workgroup selection)
+    print(f"layer sigmoid NaN row E={n_exp}", flush=True)
+    run_layer(720 + n_exp, 256, 512, n_exp, 4, 1, "sigmoid", shared=False, use_bias=True,
+              nan_rows=(1, 5))
 
 
 def test_repeated_calls_bit_identical_with_zeros():

@@ -28,13 +28,15 @@
  *             h' = w_route * silu(g) * u in fp16, already permuted for the
  *             down kernel.
  *   down    : grid (hidden/16 row tiles) x (unique experts x K chunks of at
- *             most 4096). Each workgroup writes its partial sums (routing weights
- *             are already folded into h').
- *   combine : adds the partials in a fixed order (shared expert, then
- *             routed experts in unique-list order, then K chunk), so the
- *             result is deterministic. A separate launch on purpose: a
- *             device-scope fence inside the down kernel costs an L2
- *             write-back per wave on this part, far more than a launch.
+ *             most 4096). Each workgroup computes its partial sums (routing
+ *             weights are already folded into h'); the last workgroup of a
+ *             row tile to arrive adds the tile's partials in a fixed order
+ *             (shared expert, then routed experts in unique-list order, then
+ *             K chunk) and writes the output, so the result is
+ *             deterministic. The hand-off uses device-coherent stores and
+ *             loads of the partials plus an arrival counter, not a fence: a
+ *             device-scope fence writes back the whole L2 on this part, far
+ *             more costly than the few partials involved.
  *
  * Weights are read once, in place, from the reference blob layout
  * (csrc/core/wisp_engine.h:214-238); nothing is dequantised to memory.
@@ -65,6 +67,7 @@ struct DecodeParams {
     uint16_t* xconv;      /* workspace copy used when the caller's x is fp32 or unaligned */
     uint16_t* hperm;      /* [max_u][M][inter] permuted fp16 h'           */
     float* part;          /* [max_u][n_chunks][M][hidden] down partials   */
+    int* tile_cnt;        /* [hidden / 16] down workgroups arrived per row tile */
     float* out32;         /* [M][hidden] layer output (either may be null) */
     uint16_t* out16;
     int accumulate;
@@ -116,6 +119,7 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
 
     for (int e = threadIdx.x; e < n_experts; e += blockDim.x) s_tab[e] = (const uint8_t*)table[e];
+    for (int i = threadIdx.x; i < P.hidden / 16; i += blockDim.x) P.tile_cnt[i] = 0;
     /* x -> fp16 copy when the gate/up kernel cannot read the caller's x */
     if (P.xconv) {
         for (int i = threadIdx.x; i < M * P.hidden; i += blockDim.x)
@@ -147,6 +151,35 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
                                    bias ? half_bits_to_float(bias[e]) : 0.0f);
             }
             __syncthreads();
+        }
+        if (M == 1 && n_experts <= 64) {
+            /* one token, few experts: wave 0 selects and builds the unique
+             * list (the selection is distinct) without another barrier */
+            if (wv != 0) return;
+            int e;
+            float w;
+            topk_wave_small(s_sc, R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr, R.logits,
+                            n_experts, top_k, R.kind, e, w);
+            const int base = shared_blob ? 1 : 0;
+            const bool valid = lane < top_k && e >= 0;
+            const uint64_t m = __ballot(valid);
+            if (lane < top_k) {
+                R.idx[lane] = e;
+                R.w[lane] = w;
+            }
+            if (valid) {
+                const int slot = base + __popcll(m & ((1ull << lane) - 1ull));
+                P.ublob[slot] = s_tab[e];
+                for (int v = 0; v < DEC_MAX_TOKENS; v++) P.uw[slot * 4 + v] = v == 0 ? w : 0.0f;
+            }
+            if (lane == 0) {
+                *P.n_unique = base + __popcll(m);
+                if (shared_blob) {
+                    P.ublob[0] = (const uint8_t*)shared_blob;
+                    for (int v = 0; v < DEC_MAX_TOKENS; v++) P.uw[v] = v == 0 ? 1.0f : 0.0f;
+                }
+            }
+            return;
         }
         for (int t = 0; t < M; t++)
             topk_block(s_sc + t * n_experts, R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr, s_ck,
@@ -555,20 +588,42 @@ __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void gateup_kernel(const Decode
 /* down (per expert and K chunk) + combine                                  */
 /* ======================================================================= */
 
+/* out[v][r] (+)= y in fp32 and/or fp16. */
+__device__ __forceinline__ void store_out(const DecodeParams& P, size_t i, float y) {
+    if (P.out32) {
+        if (P.accumulate) y += P.out32[i];
+        P.out32[i] = y;
+    }
+    if (P.out16) P.out16[i] = __builtin_bit_cast(uint16_t, (f16)y);
+}
+
 /* grid (hidden / (16 TILES), max_u * n_chunks): workgroup (row tile,
- * unique expert u, K chunk c of chunk_blocks blocks) writes
+ * unique expert u, K chunk c of chunk_blocks blocks) computes
  * part[u][c][v][row] = down_u[row, chunk] . h'_u[v][chunk] (routing weight
- * already folded into h'). */
+ * already folded into h'). The last of the row tile's n_unique * n_chunks
+ * workgroups to arrive adds all of the tile's partials in a fixed order
+ * (shared expert, then routed experts in unique-list order, then K chunk)
+ * and writes the output, so the result is deterministic. The hand-off needs
+ * no cache write-back: partials are stored and loaded with device-coherent
+ * accesses, every store is acknowledged before the arrival is counted, and
+ * the counters are zeroed by the prep kernel of the same call. */
 template <int M, int NG, int TILES, int NB, bool HZ>
 __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void down_kernel(const DecodeParams P) {
     constexpr int NT = TILES;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ int s_last;
     const int nch = P.n_chunks;
     const int u = blockIdx.y / nch, c = blockIdx.y - u * nch;
     const int r0 = blockIdx.x * 16 * TILES;
     const int n_u = *P.n_unique;
     const uint8_t* blob = P.ublob[u];
-    if (u >= n_u) return;
+    if (u >= n_u) {
+        /* nothing routed: one workgroup per row tile writes the empty sum */
+        if (n_u == 0 && blockIdx.y == 0)
+            for (int o = threadIdx.x; o < TILES * 16 * M; o += blockDim.x)
+                store_out(P, (size_t)(o / (16 * TILES)) * P.hidden + r0 + o % (16 * TILES), 0.0f);
+        return;
+    }
     const int K = P.inter, H = P.hidden;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int col = lane & 15, j = lane >> 4;
@@ -651,34 +706,35 @@ __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void down_kernel(const DecodePa
         const int v = o % M, rc = o / M, q = rc / 16, cc = rc % 16;
         float y = 0.0f;
         for (int ww = 0; ww < nw; ww++) y += red[((ww * NT + q) * 16 + cc) * M + v];
-        P.part[(((size_t)u * nch + c) * M + v) * H + r0 + 16 * q + cc] = y;
+        __hip_atomic_store(P.part + (((size_t)u * nch + c) * M + v) * H + r0 + 16 * q + cc, y,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-}
-
-/* out[v][r] (+)= sum over unique experts u (list order) and K chunks c of
- * part[u][c][v][r]. All loads of a thread are issued before the sum. */
-__global__ __launch_bounds__(256) void combine_kernel(const DecodeParams P) {
+    __builtin_amdgcn_s_waitcnt(0);   /* this thread's partial stores are acknowledged */
+    __syncthreads();
+    const int n_q = n_u * nch;
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(P.tile_cnt + blockIdx.x, 1, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT) == n_q - 1;
+    __syncthreads();
+    if (!s_last) return;
     constexpr int MAXQ = 16;
-    const int n_q = *P.n_unique * P.n_chunks;
-    const int H = P.hidden;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= P.M * H) return;
-    const int v = i / H, r = i - v * H;
-    const size_t stride = (size_t)P.M * H;
-    const float* src = P.part + (size_t)v * H + r;
-    float y = 0.0f;
-    for (int q0 = 0; q0 < n_q; q0 += MAXQ) {
-        float t[MAXQ];
+    for (int o = threadIdx.x; o < TILES * 16 * M; o += blockDim.x) {
+        const int v = o / (16 * TILES), r = r0 + o % (16 * TILES);
+        const float* src = P.part + (size_t)v * H + r;
+        const size_t stride = (size_t)M * H;
+        float y = 0.0f;
+        for (int q0 = 0; q0 < n_q; q0 += MAXQ) {
+            float t[MAXQ];
 #pragma unroll
-        for (int q = 0; q < MAXQ; q++) t[q] = (q0 + q < n_q) ? src[(size_t)(q0 + q) * stride] : 0.0f;
+            for (int q = 0; q < MAXQ; q++)
+                t[q] = q0 + q < n_q ? __hip_atomic_load(src + (size_t)(q0 + q) * stride,
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                    : 0.0f;
 #pragma unroll
-        for (int q = 0; q < MAXQ; q++) y += t[q];
+            for (int q = 0; q < MAXQ; q++) y += t[q];
+        }
+        store_out(P, (size_t)v * H + r, y);
     }
-    if (P.out32) {
-        if (P.accumulate) y += P.out32[i];
-        P.out32[i] = y;
-    }
-    if (P.out16) P.out16[i] = __builtin_bit_cast(uint16_t, (f16)y);
 }
 
 /* ======================================================================= */
@@ -698,7 +754,10 @@ extern "C" hipError_t wisp_expert_layout_check(const WispExpertLayout* L) {
     if (!gs_ok || hidden % gs || inter % gs) return hipErrorInvalidValue;
     for (int m = 0; m < 3; m++) {
         const uint64_t n = (uint64_t)L->rows[m] * L->cols[m];
-        if ((L->packed_off[m] + 8) % 16) return hipErrorInvalidValue;
+        /* blobs sit at 8 mod 16 (the reference's 120-byte header then
+         * contiguous sections): every section starts 16-byte aligned */
+        if ((L->packed_off[m] + 8) % 16 || (L->scales_off[m] + 8) % 16) return hipErrorInvalidValue;
+        if (L->has_zeros && (L->zeros_off[m] + 8) % 16) return hipErrorInvalidValue;
         if (L->scales_off[m] < L->packed_off[m] + n / 2) return hipErrorInvalidValue;
         if (L->scales_off[m] % 2 || L->zeros_off[m] % 2) return hipErrorInvalidValue;
         if (L->has_zeros && L->zeros_off[m] < L->scales_off[m] + n / gs * 2)
@@ -718,7 +777,7 @@ static int dec_chunk_blocks(int nblk) {
 }
 
 struct WsLayout {
-    size_t nu, ublob, uw, xconv, hperm, part, total;
+    size_t nu, tile_cnt, ublob, uw, xconv, hperm, part, total;
     int max_u;
 };
 
@@ -727,6 +786,7 @@ static WsLayout ws_layout(const WispExpertLayout* L, int M, int top_k, int has_s
     w.max_u = (has_shared ? 1 : 0) + M * top_k;
     size_t off = 0;
     w.nu = off; off += 256;
+    w.tile_cnt = off; off = align_up(off + (size_t)(L->cols[0] / 16) * sizeof(int), 256);
     w.ublob = off; off = align_up(off + (size_t)w.max_u * sizeof(void*), 256);
     w.uw = off; off = align_up(off + (size_t)w.max_u * 4 * sizeof(float), 256);
     w.xconv = off; off = align_up(off + (size_t)M * L->cols[0] * 2, 256);
@@ -783,9 +843,6 @@ static void launch_compute(const DecodeParams& P, hipStream_t s) {
     ev_before(EV_DOWN, s);
     launch_down<M, NG, 1, 8, HZ>(P, s);
     ev_after(EV_DOWN, s);
-    ev_before(EV_COMBINE, s);
-    hipLaunchKernelGGL(combine_kernel, dim3((M * P.hidden + 255) / 256), dim3(256), 0, s, P);
-    ev_after(EV_COMBINE, s);
 }
 
 template <int M>
@@ -838,6 +895,7 @@ static hipError_t decode_run(const void* const* d_expert_table, const void* d_sh
     P.M = M;
     char* ws = (char*)d_workspace;
     P.n_unique = (int*)(ws + w.nu);
+    P.tile_cnt = (int*)(ws + w.tile_cnt);
     P.ublob = (const uint8_t**)(ws + w.ublob);
     P.uw = (float*)(ws + w.uw);
     const bool x_direct = x_dtype == WISP_DTYPE_F16 && ((uintptr_t)d_x % 16) == 0;

@@ -139,6 +139,57 @@ __device__ __forceinline__ uint64_t route_composite(float key, int e) {
 
 typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
 
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int lane) {
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+/* One wave, n_experts <= 64, one token: the selection topk_block makes,
+ * with the same arithmetic in the same order (so the same bits), but
+ * every reduction in registers: no LDS and no barrier. lg: the token's raw
+ * logits (LDS or global). Writes scores_out[e]; lane q < top_k returns the
+ * q-th selection in sel_e (-1 past the candidates) and its renormalised
+ * weight in sel_w. */
+__device__ __forceinline__ void topk_wave_small(const float* lg, const uint16_t* __restrict__ bias,
+                                                float* scores_out, int n_experts, int top_k,
+                                                int kind, int& sel_e, float& sel_w) {
+    const bool sig = kind == WISP_ROUTER_SIGMOID;
+    const int lane = threadIdx.x & 63;
+    const bool act = lane < n_experts;
+    const float l = act ? lg[lane] : -INFINITY;
+    float key = l;
+    if (act && sig && bias) key = 1.0f / (1.0f + __expf(-l)) + half_bits_to_float(bias[lane]);
+    const uint64_t ce = act ? route_composite(key, lane) : 0ull;
+    float mx = l;
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, WAVE));
+    const float v = act ? (sig ? 1.0f / (1.0f + __expf(-l)) : __expf(l - mx)) : 0.0f;
+    const float denom = wave_sum(v);
+    const float inv = 1.0f / (denom > 0.0f ? denom : 1.0f);
+    const float score = sig ? v : v * inv;
+    if (act) scores_out[lane] = score;
+    int rank = 0;
+    for (int j = 0; j < n_experts; j++) rank += readlane64(ce, j) > ce;
+    const bool picked = act && (ce >> 32) != 0 && rank < top_k;
+    /* lane q takes the expert of rank q */
+    sel_e = -1;
+    sel_w = 0.0f;
+    for (int q = 0; q < top_k; q++) {
+        const uint64_t m = __ballot(picked && rank == q);
+        if (m) {
+            const int src = __builtin_ctzll(m);
+            const float sv = __shfl(score, src, WAVE);
+            if (lane == q) {
+                sel_e = src;
+                sel_w = sv;
+            }
+        }
+    }
+    float wsum = 0.0f;
+    for (int q = 0; q < top_k; q++) wsum += __shfl(sel_w, q, WAVE);
+    if (wsum > 0.0f) sel_w /= wsum;
+}
+
 /* All threads of the workgroup, one token. lg: the token's raw logits
  * [n_experts] (LDS or global; for SOFTMAX they already include the bias).
  * s_ck: LDS scratch of n_experts uint64, 16-byte aligned; s_sc: LDS
