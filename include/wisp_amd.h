@@ -195,10 +195,11 @@ hipError_t wisp_gpu_moe_scatter(const float* d_y, const int* d_inv,
  *    A one-workgroup prep kernel (unique-expert list, routing weights),
  *    then (a) gate+up+SiLU over every unique expert touched by the M tokens
  *    in one launch, (b) the down projections of all of them in one launch,
- *    (c) a fixed-order combine of the per-expert partials (routing weights
- *    are folded in before the down projection). Weights stream from the
- *    blobs in place; nothing is dequantised to memory. Routing stays on
- *    the device.
+ *    whose last workgroup per output row tile adds the per-expert partials
+ *    in a fixed order (routing weights are folded in before the down
+ *    projection), so repeated calls give identical bits. Weights stream
+ *    from the blobs in place; nothing is dequantised to memory. Routing
+ *    stays on the device.
  * ======================================================================= */
 
 enum { WISP_DTYPE_F16 = 0, WISP_DTYPE_F32 = 1 };
@@ -232,7 +233,7 @@ hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table,
  * trip: router logits = W x (+ bias), softmax or sigmoid top-k with the
  * rules of wisp_gpu_moe_route, then everything wisp_gpu_moe_decode_int4
  * does. The router GEMV runs inside the prep kernel when W is at most
- * 256 KiB (4 launches per layer), else in one launch before it. Writes the
+ * 256 KiB (3 launches per layer), else in one launch before it. Writes the
  * post-activation scores [n_tokens, n_experts] to d_scores and the
  * selection [n_tokens, top_k] to d_topk_idx / d_topk_w (device), as
  * wisp_gpu_moe_route does. Workspace: wisp_moe_decode_workspace_bytes.
