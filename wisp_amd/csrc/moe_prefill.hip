@@ -36,9 +36,8 @@
 #include "hip_common.h"
 
 #define PF_BM 128                 /* tokens per tile                         */
-#define PF_NT 4                   /* 16-row weight tiles per wave            */
-#define PF_WAVES 4
-#define PF_THREADS (64 * PF_WAVES)
+#define PF_WAVES 8                /* waves of the <= 32 and <= 64 token classes */
+#define PF_WAVES_LARGE 8          /* waves of the <= 128 token class            */
 #define PF_AROW 136               /* LDS A row stride in halves (128 + 8)    */
 #define PF_MAX_EXPERTS 4096
 #define PF_CLASSES 3              /* tiles of <= 32, <= 64, <= 128 tokens    */
@@ -165,22 +164,28 @@ __device__ __forceinline__ h8 dequant8(uint32_t w, h2 s2, h2 z2) {
     return __builtin_bit_cast(h8, o);
 }
 
-/* grid (tiles of class CLS, n-blocks). GATEUP: the workgroup covers h
- * features [128 by, 128 by + 128): wave w owns gate rows f0 .. f0 + 31 and
- * up rows f0 .. f0 + 31 with f0 = 128 by + 32 w (row tiles s = 0,1 gate,
- * 2,3 up). DOWN: output rows [256 by, +256): wave w owns 4 row tiles from
- * 256 by + 64 w. K = hidden (GATEUP) or inter (DOWN) in 128-wide blocks.
- * TV: 16-token sub-tiles of the class (rows past the tile's count are
- * zeros); R: weight blocks held in the register ring (R - 1 in flight
- * while one is computed).
+/* grid (tiles of class CLS, n-blocks); WV waves, each owning NT = 16 / WV
+ * row tiles of 16 weight rows. GATEUP: the workgroup covers h features
+ * [128 by, 128 by + 128): wave w owns gate rows f0 .. f0 + 8 NT - 1 and the
+ * same up rows, f0 = 128 by + (128 / WV) w (row tiles s < NT/2 gate, the
+ * rest up). DOWN: output rows [256 by, +256): wave w owns NT row tiles from
+ * 256 by + (256 / WV) w. K = hidden (GATEUP) or inter (DOWN) in 128-wide
+ * blocks. TV: 16-token sub-tiles of the class (rows past the tile's count
+ * are zeros); R: weight blocks held in the register ring (R - 1 in flight
+ * while one is computed). Eight waves with half the rows each halve the
+ * accumulator and ring registers, so two waves fit on a SIMD and one
+ * wave's dequant overlaps another's MFMAs.
  *
  * Pipeline of step b: commit the A tile of block b + 1 (loaded during step
  * b - 1) to the other LDS buffer, issue the A loads of block b + 2, issue
  * the weights of block b + R - 1, compute block b, barrier. */
-template <bool GATEUP, bool HZ, int TV, int R>
-__global__ __launch_bounds__(PF_THREADS) void pf_gemm_kernel(const PfParams P, int cls) {
+template <bool GATEUP, bool HZ, int TV, int R, int WV>
+__global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int cls) {
+    constexpr int THREADS = 64 * WV;
+    constexpr int NT = 16 / WV;                  /* 16-row weight tiles per wave */
     constexpr int BM = 16 * TV;
-    constexpr int APT = BM * 16 / PF_THREADS;   /* A pieces (16 B) per thread per block */
+    constexpr int APT = BM * 16 / THREADS;       /* A pieces (16 B) per thread per block */
+    static_assert(APT >= 1 && APT * THREADS == BM * 16, "A staging must divide evenly");
     __shared__ __attribute__((aligned(16))) uint16_t s_a[2][BM * PF_AROW];
     __shared__ int s_row[BM];      /* source row of each tile row (-1: none) */
     __shared__ float s_wr[BM];     /* routing weight of each tile row        */
@@ -196,7 +201,7 @@ __global__ __launch_bounds__(PF_THREADS) void pf_gemm_kernel(const PfParams P, i
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, j = lane >> 4;
 
-    for (int r = threadIdx.x; r < BM; r += PF_THREADS) {
+    for (int r = threadIdx.x; r < BM; r += THREADS) {
         if (r < nv) {
             const int pair = P.order[p0 + r];
             s_row[r] = GATEUP ? pair / P.top_k1 : p0 + r;
@@ -208,18 +213,18 @@ __global__ __launch_bounds__(PF_THREADS) void pf_gemm_kernel(const PfParams P, i
     }
 
     /* weight row tiles of this wave */
-    const uint8_t* wp[PF_NT];
-    const uint16_t* sp[PF_NT];
-    const uint16_t* zp[PF_NT];
+    const uint8_t* wp[NT];
+    const uint16_t* sp[NT];
+    const uint16_t* zp[NT];
 #pragma unroll
-    for (int s = 0; s < PF_NT; s++) {
+    for (int s = 0; s < NT; s++) {
         int mat, row;
         if (GATEUP) {
-            mat = s < 2 ? 0 : 1;
-            row = blockIdx.y * 128 + wave * 32 + 16 * (s & 1) + col;
+            mat = s < NT / 2 ? 0 : 1;
+            row = blockIdx.y * 128 + wave * (128 / WV) + 16 * (s % (NT / 2)) + col;
         } else {
             mat = 2;
-            row = blockIdx.y * 256 + wave * 64 + 16 * s + col;
+            row = blockIdx.y * 256 + wave * (256 / WV) + 16 * s + col;
         }
         wp[s] = blob + P.p_off[mat] + (size_t)row * (K / 2) + 16 * j;
         sp[s] = (const uint16_t*)(blob + P.s_off[mat]) + (size_t)row * G;
@@ -228,11 +233,11 @@ __global__ __launch_bounds__(PF_THREADS) void pf_gemm_kernel(const PfParams P, i
     /* group of this lane's 32 K values in block b: (128 b + 32 j) / gs */
     const int gshift = 31 - __builtin_clz(P.gs);
 
-    f4 acc[TV][PF_NT];
+    f4 acc[TV][NT];
 #pragma unroll
     for (int t = 0; t < TV; t++)
 #pragma unroll
-        for (int s = 0; s < PF_NT; s++) acc[t][s] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s = 0; s < NT; s++) acc[t][s] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
 
     __syncthreads();   /* s_row visible */
 
@@ -242,7 +247,7 @@ __global__ __launch_bounds__(PF_THREADS) void pf_gemm_kernel(const PfParams P, i
     int aoff[APT];     /* element offset of each piece's source row (-1: zero) */
 #pragma unroll
     for (int c = 0; c < APT; c++) {
-        const int i = threadIdx.x + c * PF_THREADS;
+        const int i = threadIdx.x + c * THREADS;
         const int src = s_row[i >> 4];
         aoff[c] = src >= 0 ? src * K + 8 * (i & 15) : -1;
     }
@@ -255,19 +260,19 @@ __global__ __launch_bounds__(PF_THREADS) void pf_gemm_kernel(const PfParams P, i
     auto a_commit = [&](int buf) {
 #pragma unroll
         for (int c = 0; c < APT; c++) {
-            const int i = threadIdx.x + c * PF_THREADS;
+            const int i = threadIdx.x + c * THREADS;
             *(u4*)(&s_a[buf][(i >> 4) * PF_AROW + 8 * (i & 15)]) = perm8_halves(areg[c]);
         }
     };
 
     /* weight ring: block b lives in slot b % R */
-    u4 wr[R][PF_NT];
-    uint16_t sr[R][PF_NT], zr[R][PF_NT];
+    u4 wr[R][NT];
+    uint16_t sr[R][NT], zr[R][NT];
     auto w_issue = [&](int slot, int b) {
         const int bb = min(b, nblk - 1);
         const int g = (bb * 128 + 32 * j) >> gshift;
 #pragma unroll
-        for (int s = 0; s < PF_NT; s++) {
+        for (int s = 0; s < NT; s++) {
             wr[slot][s] = *(const u4*)(wp[s] + (size_t)bb * 64);
             sr[slot][s] = sp[s][g];
             if (HZ) zr[slot][s] = zp[s][g];
@@ -297,7 +302,7 @@ __global__ __launch_bounds__(PF_THREADS) void pf_gemm_kernel(const PfParams P, i
                     for (int t = 0; t < TV; t++)
                         af[t] = *(const h8*)(abuf + (16 * t + col) * PF_AROW + 32 * j + 8 * kk);
 #pragma unroll
-                    for (int s = 0; s < PF_NT; s++) {
+                    for (int s = 0; s < NT; s++) {
                         const f16 sc = __builtin_bit_cast(f16, sr[r][s]);
                         const f16 zc = HZ ? __builtin_bit_cast(f16, zr[r][s]) : (f16)0.0f;
                         const h8 bf = dequant8<HZ>(wr[r][s][kk], (h2){sc, sc}, (h2){zc, zc});
@@ -320,16 +325,16 @@ __global__ __launch_bounds__(PF_THREADS) void pf_gemm_kernel(const PfParams P, i
                 if (GATEUP) {
                     const float wrt = s_wr[r];
 #pragma unroll
-                    for (int s = 0; s < 2; s++) {
-                        const float g = acc[t][s][v], u = acc[t][2 + s][v];
+                    for (int s = 0; s < NT / 2; s++) {
+                        const float g = acc[t][s][v], u = acc[t][NT / 2 + s][v];
                         const float h = silu_f(g) * u * wrt;
-                        const int c = blockIdx.y * 128 + wave * 32 + 16 * s + col;
+                        const int c = blockIdx.y * 128 + wave * (128 / WV) + 16 * s + col;
                         P.H[(size_t)(p0 + r) * P.inter + c] = __builtin_bit_cast(uint16_t, (f16)h);
                     }
                 } else {
 #pragma unroll
-                    for (int s = 0; s < PF_NT; s++) {
-                        const int c = blockIdx.y * 256 + wave * 64 + 16 * s + col;
+                    for (int s = 0; s < NT; s++) {
+                        const int c = blockIdx.y * 256 + wave * (256 / WV) + 16 * s + col;
                         P.Y[(size_t)(p0 + r) * P.hidden + c] =
                             __builtin_bit_cast(uint16_t, (f16)acc[t][s][v]);
                     }
@@ -426,12 +431,12 @@ extern "C" size_t wisp_moe_prefill_workspace_bytes(const WispExpertLayout* L, in
 template <bool GATEUP, bool HZ>
 static void pf_launch(const PfParams& P, const int* gx, hipStream_t s) {
     const int ny = GATEUP ? P.inter / 128 : P.hidden / 256;
-    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 8, 3>), dim3(gx[2], ny), dim3(PF_THREADS), 0, s,
-                       P, 2);
-    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 4, 4>), dim3(gx[1], ny), dim3(PF_THREADS), 0, s,
-                       P, 1);
-    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 2, 6>), dim3(gx[0], ny), dim3(PF_THREADS), 0, s,
-                       P, 0);
+    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 8, 3, PF_WAVES_LARGE>), dim3(gx[2], ny),
+                       dim3(64 * PF_WAVES_LARGE), 0, s, P, 2);
+    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 4, 4, PF_WAVES>), dim3(gx[1], ny),
+                       dim3(64 * PF_WAVES), 0, s, P, 1);
+    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 2, 6, PF_WAVES>), dim3(gx[0], ny),
+                       dim3(64 * PF_WAVES), 0, s, P, 0);
 }
 
 extern "C" hipError_t wisp_gpu_expert_offsets(const int* d_topk_idx, int n_tokens, int top_k,
