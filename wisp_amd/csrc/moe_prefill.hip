@@ -36,8 +36,8 @@
 #include "hip_common.h"
 
 #define PF_BM 128                 /* tokens per tile                         */
-#define PF_WAVES 8                /* waves of the <= 32 and <= 64 token classes */
-#define PF_WAVES_LARGE 8          /* waves of the <= 128 token class            */
+#define PF_WAVES 8                /* waves per workgroup (NT = 2 row tiles each) */
+#define PF_RING 4                 /* weight blocks in the register ring (3 in flight) */
 #define PF_AROW 136               /* LDS A row stride in halves (128 + 8)    */
 #define PF_MAX_EXPERTS 4096
 #define PF_CLASSES 3              /* tiles of <= 32, <= 64, <= 128 tokens    */
@@ -425,17 +425,17 @@ extern "C" size_t wisp_moe_prefill_workspace_bytes(const WispExpertLayout* L, in
     return pf_ws_layout(L, n_tokens, top_k, n_experts, has_shared).total;
 }
 
-/* One launch per tile class (sub-tiles per tile 2 / 4 / 8, weight ring
- * 6 / 4 / 3 blocks: the memory-bound small tiles keep more weight blocks in
- * flight, the MFMA-bound large ones spend the registers on accumulators). */
+/* One launch per tile class (sub-tiles per tile 2 / 4 / 8), each with its
+ * own register budget; eight waves and a ring of four weight blocks measured
+ * best for every class on MI355X (deeper rings cost occupancy). */
 template <bool GATEUP, bool HZ>
 static void pf_launch(const PfParams& P, const int* gx, hipStream_t s) {
     const int ny = GATEUP ? P.inter / 128 : P.hidden / 256;
-    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 8, 3, PF_WAVES_LARGE>), dim3(gx[2], ny),
-                       dim3(64 * PF_WAVES_LARGE), 0, s, P, 2);
-    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 4, 4, PF_WAVES>), dim3(gx[1], ny),
+    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 8, PF_RING, PF_WAVES>), dim3(gx[2], ny),
+                       dim3(64 * PF_WAVES), 0, s, P, 2);
+    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 4, PF_RING, PF_WAVES>), dim3(gx[1], ny),
                        dim3(64 * PF_WAVES), 0, s, P, 1);
-    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 2, 6, PF_WAVES>), dim3(gx[0], ny),
+    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 2, PF_RING, PF_WAVES>), dim3(gx[0], ny),
                        dim3(64 * PF_WAVES), 0, s, P, 0);
 }
 
