@@ -152,14 +152,9 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
             }
             __syncthreads();
         }
-        if (M == 1 && n_experts <= 64) {
-            /* one token, few experts: wave 0 selects and builds the unique
-             * list (the selection is distinct) without another barrier */
-            if (wv != 0) return;
-            int e;
-            float w;
-            topk_wave_small(s_sc, R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr, R.logits,
-                            n_experts, top_k, R.kind, e, w);
+        /* One token: the selection is distinct, so wave 0 writes it and the
+         * unique list directly (shared expert first, then rank order). */
+        auto one_token_list = [&](int e, float w) {
             const int base = shared_blob ? 1 : 0;
             const bool valid = lane < top_k && e >= 0;
             const uint64_t m = __ballot(valid);
@@ -179,12 +174,26 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
                     for (int v = 0; v < DEC_MAX_TOKENS; v++) P.uw[v] = v == 0 ? 1.0f : 0.0f;
                 }
             }
+        };
+        if (M == 1 && n_experts <= 64) {
+            /* few experts: wave 0 selects in registers, no further barrier */
+            if (wv != 0) return;
+            int e;
+            float w;
+            topk_wave_small(s_sc, R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr, R.logits,
+                            n_experts, top_k, R.kind, e, w);
+            one_token_list(e, w);
             return;
         }
         for (int t = 0; t < M; t++)
             topk_block(s_sc + t * n_experts, R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr, s_ck,
                        s_sc + t * n_experts, s_red, R.logits + (size_t)t * n_experts, n_experts,
                        top_k, R.kind, s_e + t * top_k, s_w + t * top_k);
+        if (M == 1) {
+            if (wv != 0) return;
+            one_token_list(lane < top_k ? s_e[lane] : -1, lane < top_k ? s_w[lane] : 0.0f);
+            return;
+        }
     } else {
         for (int p = threadIdx.x; p < n_pairs; p += blockDim.x) {
             s_e[p] = R.idx[p];

@@ -33,9 +33,24 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
     XT* xs = (XT*)lds_raw;
     const int t0 = blockIdx.y * ROUTE_TOK_PER_WG;
     const int nt = min(ROUTE_TOK_PER_WG, n_tokens - t0);
+    const int lane = threadIdx.x & 63;
+    if (hidden <= ROUTE_UNROLL * WAVE * 8 && gridDim.x * 4 >= n_experts) {
+        /* one row per wave: its loads go out before the token rows are
+         * staged, so the kernel costs one memory round trip */
+        const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+        u4 wrow[ROUTE_UNROLL];
+        if (e < n_experts) router_row_load(W + (size_t)e * hidden, hidden, lane, wrow);
+        stage_rows<XT>(xs, x + (size_t)t0 * hidden, nt, hidden);
+        __syncthreads();
+        if (e < n_experts) {
+            const float b = (add_bias && bias) ? half_bits_to_float(bias[e]) : 0.0f;
+            router_row_fma<XT>(wrow, xs, nt, hidden, lane, logits + (size_t)t0 * n_experts + e,
+                               n_experts, b);
+        }
+        return;
+    }
     stage_rows<XT>(xs, x + (size_t)t0 * hidden, nt, hidden);
     __syncthreads();
-    const int lane = threadIdx.x & 63;
     for (int e = blockIdx.x * 4 + (threadIdx.x >> 6); e < n_experts; e += gridDim.x * 4) {
         float acc[ROUTE_TOK_PER_WG];
         router_row_dot<XT>(W + (size_t)e * hidden, xs, nt, hidden, lane, acc);

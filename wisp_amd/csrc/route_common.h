@@ -273,16 +273,17 @@ __device__ __forceinline__ void topk_block(const float* lg, const uint16_t* __re
         if (h == 0 && e < n_experts && (ce >> 32) != 0 && rank < top_k) out_idx[rank] = e;
     }
     __syncthreads();   /* selection and final scores visible */
-    if (tid == 0) {
-        float wsum = 0.0f;
-        for (int q = 0; q < top_k; q++) {
-            const int e = out_idx[q];
-            const float v = e >= 0 ? s_sc[e] : 0.0f;
-            out_w[q] = v;
-            wsum += v;
+    if (wv == 0) {
+        /* lane q gathers the q-th weight; the sum runs in rank order */
+        float v = 0.0f;
+        if (lane < top_k) {
+            const int e = out_idx[lane];
+            v = e >= 0 ? s_sc[e] : 0.0f;
         }
-        if (wsum > 0.0f)
-            for (int q = 0; q < top_k; q++) out_w[q] /= wsum;
+        float wsum = 0.0f;
+        for (int q = 0; q < top_k; q++)
+            wsum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), q));
+        if (lane < top_k) out_w[lane] = wsum > 0.0f ? v / wsum : v;
     }
     __syncthreads();
 }
