@@ -107,8 +107,9 @@ class Layer:
                                   self.out32.ptr, self.out16.ptr, self.stream.handle)
 
     def separate_router(self):
-        """True when the router GEMV gets its own launch (matrix > 256 KiB)."""
-        return self.shape.n_experts * self.shape.hidden * 2 > 256 * 1024
+        """True when the router GEMV gets its own launch: only for rows longer
+        than 8192 (otherwise it runs in router workgroups of the prep launch)."""
+        return self.shape.hidden > 8192
 
     def token_bytes(self):
         """Per pool token: algorithmic HBM bytes (packed + scales; zeros are

@@ -192,8 +192,8 @@ hipError_t wisp_gpu_moe_scatter(const float* d_y, const int* d_inv,
  *    out[t] = shared(x_t) + sum_k w[t,k] * expert_{idx[t,k]}(x_t)
  *    expert(x) = down . (silu(gate . x) * (up . x))
  *
- *    A one-workgroup prep kernel (unique-expert list, routing weights),
- *    then (a) gate+up+SiLU over every unique expert touched by the M tokens
+ *    A prep launch (unique-expert list, routing weights; with routing, the
+ *    router GEMV in workgroups of the same launch), then (a) gate+up+SiLU over every unique expert touched by the M tokens
  *    in one launch, (b) the down projections of all of them in one launch,
  *    whose last workgroup per output row tile adds the per-expert partials
  *    in a fixed order (routing weights are folded in before the down
@@ -232,8 +232,9 @@ hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table,
 /* One MoE layer for M = 1..4 tokens, routing included, with no host round
  * trip: router logits = W x (+ bias), softmax or sigmoid top-k with the
  * rules of wisp_gpu_moe_route, then everything wisp_gpu_moe_decode_int4
- * does. The router GEMV runs inside the prep kernel when W is at most
- * 256 KiB (3 launches per layer), else in one launch before it. Writes the
+ * does. The router GEMV runs in router workgroups of the prep launch
+ * (3 launches per layer) when hidden <= 8192 and W and x are 16-byte
+ * aligned, else in one launch before it. Writes the
  * post-activation scores [n_tokens, n_experts] to d_scores and the
  * selection [n_tokens, top_k] to d_topk_idx / d_topk_w (device), as
  * wisp_gpu_moe_route does. Workspace: wisp_moe_decode_workspace_bytes.

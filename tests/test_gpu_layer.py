@@ -26,6 +26,18 @@ def _keys(W, x, bias, kind):
     return np.where(np.isnan(k), -np.inf, k)
 
 
+def _scores(W, x, bias, kind):
+    """float64 post-activation router scores of one token (softmax over the
+    biased logits, or the sigmoid of the raw logits)."""
+    l = W.astype(np.float64) @ x.astype(np.float64)
+    if kind == "softmax":
+        if bias is not None:
+            l = l + bias.astype(np.float64)
+        z = np.exp(l - np.max(l))
+        return z / np.sum(z)
+    return 1.0 / (1.0 + np.exp(-l))
+
+
 def _near_tie(W, x, bias, kind, k):
     """True when two of the k+1 largest selection keys are too close for the
     selection to be decided by fp32 summation order (the logits' fp32 error
@@ -36,16 +48,19 @@ def _near_tie(W, x, bias, kind, k):
 
 
 def run_layer(seed, inter, hidden, n_exp, top_k, M, kind, shared, use_bias, repeat=1,
-              gs=128, zeros=False, nan_rows=()):
+              gs=128, zeros=False, nan_rows=(), vary_x=False, x32=False):
+    """One workspace, `repeat` calls. With vary_x every call routes new tokens
+    and each call's output is checked; otherwise the calls repeat one input
+    and must agree bit for bit."""
     rng = np.random.default_rng(seed)
     W = synth.make_router(rng, n_exp, hidden, std=0.05)
     for r in nan_rows:
         W[r] = np.float16("nan")
     bias = (rng.standard_normal(n_exp) * 0.1).astype(np.float16) if use_bias else None
-    x = synth.make_x(rng, M, hidden)
+    xs = [synth.make_x(rng, M, hidden) for _ in range(repeat if vary_x else 1)]
     # upload only the experts the routing can reach: each token's k + 4 best
     # keys (the slots of the others are never read)
-    cand = sorted({int(e) for t in range(M)
+    cand = sorted({int(e) for x in xs for t in range(M)
                    for e in np.argsort(-_keys(W, x[t], bias, kind))[: top_k + 4]})
     arena = moe.ExpertArena(n_exp, inter, hidden, gs,
                             lambda e, out: make_expert(seed, e, inter, hidden, gs, zeros, out),
@@ -55,46 +70,54 @@ def run_layer(seed, inter, hidden, n_exp, top_k, M, kind, shared, use_bias, repe
     if shared:
         sh_dev = DeviceBuffer(sh_blob.nbytes + 16)
         sh_dev.upload(sh_blob, offset=8)
-    dW, dx = to_device(W), to_device(x)
+    dW = to_device(W)
+    dxs = [to_device(x.astype(np.float32) if x32 else x) for x in xs]
     db = to_device(bias) if use_bias else None
     sc, di, dw = DeviceBuffer(4 * M * n_exp), DeviceBuffer(4 * M * top_k), DeviceBuffer(4 * M * top_k)
     ws = DeviceBuffer(moe.decode_workspace_bytes(arena.layout, M, top_k, shared))
     out32, out16 = DeviceBuffer(4 * M * hidden), DeviceBuffer(2 * M * hidden)
     kcode = moe.ROUTER_SOFTMAX if kind == "softmax" else moe.ROUTER_SIGMOID
+    blobs = [arena.host.get(e, arena.host[cand[0]]) for e in range(n_exp)]
+
+    def check(x, g32, g16, gi, gw, gs):
+        for t in range(M):
+            # the scores output of every expert
+            assert np.allclose(gs[t], _scores(W, x[t], bias, kind), rtol=1e-4, atol=1e-7,
+                               equal_nan=True), t
+            oi, ow, _ = O.router_topk(W.view(np.uint16), bias.view(np.uint16) if use_bias else None,
+                                      x[t].astype(np.float32), top_k, kind=kind)
+            if _near_tie(W, x[t], bias, kind, top_k):
+                # selection decided by rounding: check the experts' math on the
+                # device's own selection instead
+                assert set(gi[t].tolist()) <= set(cand)
+                oi, ow = gi[t], gw[t]
+            else:
+                assert set(oi.tolist()) <= set(cand)
+                assert gi[t].tolist() == oi.tolist(), (t, gi[t], oi)
+                assert np.allclose(gw[t], ow, rtol=1e-4, atol=1e-6), (t, gw[t], ow)
+            assert not set(gi[t].tolist()) & set(nan_rows), (t, gi[t])
+            want = O.moe_combine(blobs, sh_blob, x[t].astype(np.float32), oi, ow)
+            assert_close(g32[t], want, f"token {t} fp32")
+            assert_close(g16[t], want, f"token {t} fp16")
+
     results = []
-    for _ in range(repeat):
+    for i in range(repeat):
+        xi = i if vary_x else 0
         moe.moe_layer_decode_int4(dW.ptr, db.ptr if use_bias else 0, kcode, sc.ptr, di.ptr, dw.ptr,
                                   arena.table.ptr, sh_dev.ptr + 8 if shared else 0, arena.layout,
-                                  dx.ptr, M, top_k, n_exp, ws, out32.ptr, out16.ptr)
+                                  dxs[xi].ptr, M, top_k, n_exp, ws, out32.ptr, out16.ptr,
+                                  x_dtype=moe.DTYPE_F32 if x32 else moe.DTYPE_F16)
         synchronize()
-        results.append(out32.download(np.float32, (M, hidden)))
-    g32 = results[-1]
-    g16 = out16.download(np.float16, (M, hidden)).astype(np.float32)
-    gi = di.download(np.int32, (M, top_k))
-    gw = dw.download(np.float32, (M, top_k))
-    blobs = [arena.host.get(e, arena.host[cand[0]]) for e in range(n_exp)]
-    checked = 0
-    for t in range(M):
-        oi, ow, _ = O.router_topk(W.view(np.uint16), bias.view(np.uint16) if use_bias else None,
-                                  x[t].astype(np.float32), top_k, kind=kind)
-        if _near_tie(W, x[t], bias, kind, top_k):
-            # selection decided by rounding: check the experts' math on the
-            # device's own selection instead
-            assert set(gi[t].tolist()) <= set(cand)
-            oi, ow = gi[t], gw[t]
-        else:
-            assert set(oi.tolist()) <= set(cand)
-            assert gi[t].tolist() == oi.tolist(), (t, gi[t], oi)
-            assert np.allclose(gw[t], ow, rtol=1e-4, atol=1e-6), (t, gw[t], ow)
-        assert not set(gi[t].tolist()) & set(nan_rows), (t, gi[t])
-        want = O.moe_combine(blobs, sh_blob, x[t].astype(np.float32), oi, ow)
-        assert_close(g32[t], want, f"token {t} fp32")
-        assert_close(g16[t], want, f"token {t} fp16")
-        checked += 1
-    assert checked == M
-    for r in results[:-1]:
-        assert np.array_equal(r, g32), "repeated calls differ"
-    return g32
+        g32 = out32.download(np.float32, (M, hidden))
+        results.append(g32)
+        if vary_x or i == repeat - 1:
+            check(xs[xi], g32, out16.download(np.float16, (M, hidden)).astype(np.float32),
+                  di.download(np.int32, (M, top_k)), dw.download(np.float32, (M, top_k)),
+                  sc.download(np.float32, (M, n_exp)))
+    if not vary_x:
+        for r in results[:-1]:
+            assert np.array_equal(r, results[-1]), "repeated calls differ"
+    return results[-1]
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
@@ -110,17 +133,42 @@ def test_fused_router_sigmoid_bias(M):
 
 
 @pytest.mark.parametrize("kind", ["softmax", "sigmoid"])
-def test_separate_router_launch(kind):
-    # 256 experts x 1024 hidden x 2 B = 512 KiB router: logits in their own launch
-    print(f"layer {kind} separate-router", flush=True)
+def test_router_workgroups_in_prep_launch(kind):
+    # 256 experts x 1024 hidden x 2 B = 512 KiB router: logits from router
+    # workgroups of the prep launch, which the prep workgroup polls
+    print(f"layer {kind} router workgroups", flush=True)
     run_layer(700, 256, 1024, 256, 8, 3, kind, shared=True, use_bias=(kind == "sigmoid"))
 
 
-def test_one_token_64_experts_separate_router():
-    # 64 experts x 2304 hidden x 2 B = 288 KiB router: logits in their own
-    # launch, then the one-wave selection at its largest expert count
-    print("layer M=1 E=64 separate-router", flush=True)
-    run_layer(710, 256, 2304, 64, 8, 1, "softmax", shared=True, use_bias=True)
+def test_router_workgroups_consecutive_calls():
+    # each call on one workspace must select on its own tokens' logits (the
+    # routing words carry a per-call token); 60 experts x 2304 x 2 B =
+    # 276 KiB router, so 8 router workgroups, the last with 4 rows
+    print("layer router workgroups x4 calls", flush=True)
+    run_layer(705, 256, 2304, 60, 4, 4, "softmax", shared=False, use_bias=True, repeat=4,
+              vary_x=True)
+
+
+def test_router_workgroups_fp32_tokens():
+    # fp32 activations, 4 tokens, 512 experts: router workgroups of 2 rows
+    print("layer router workgroups fp32 x, E=512", flush=True)
+    run_layer(707, 256, 1024, 512, 8, 4, "sigmoid", shared=True, use_bias=True, repeat=2,
+              vary_x=True, x32=True)
+
+
+@pytest.mark.parametrize("kind", ["softmax", "sigmoid"])
+def test_separate_router_launch(kind):
+    # rows of 8320 > 8192: the logits get a launch of their own
+    print(f"layer {kind} separate-router", flush=True)
+    run_layer(730, 256, 8320, 40, 4, 2, kind, shared=True, use_bias=True, repeat=2, vary_x=True)
+
+
+def test_one_token_64_experts_router_workgroups():
+    # 64 experts x 2304 hidden x 2 B = 288 KiB router: router workgroups,
+    # then the one-wave selection at its largest expert count
+    print("layer M=1 E=64 router workgroups", flush=True)
+    run_layer(710, 256, 2304, 64, 8, 1, "softmax", shared=True, use_bias=True, repeat=3,
+              vary_x=True)
 
 
 @pytest.mark.parametrize("n_exp", [32, 256])

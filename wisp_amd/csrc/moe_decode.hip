@@ -6,9 +6,9 @@
  * expert 3 full-matrix dequants into fp16 scratch, a fused gate/up GEMV, a
  * down GEMV and a scale-accumulate) with three launches per MoE layer:
  *
- *   prep    : one workgroup. Optionally the router itself (logits, softmax
- *             or sigmoid top-k; the GEMV runs here when the router matrix is
- *             small, else in router_logits_kernel just before), then the
+ *   prep    : optionally the router (logits in router workgroups of this
+ *             launch, or in router_logits_kernel just before for rows over
+ *             8192; softmax or sigmoid top-k in the prep workgroup), then the
  *             unique-expert list of the M tokens (shared expert first, then
  *             first appearance in flat (token, slot) order) with per-(expert,
  *             token) routing weights, and the reset of the down kernel's
@@ -47,7 +47,6 @@
 #define DEC_MAX_TOPK 64
 #define DEC_MAX_WAVES 8
 #define DEC_CHUNK_MAX 32      /* down-projection K chunk per workgroup: at most 32 blocks of 128 */
-#define DEC_ROUTE_FUSE_BYTES (256 * 1024)   /* router matrices up to this size run in prep */
 #define DEC_ROUTE_MAX_EXPERTS 1024
 #define DEC_PREP_THREADS 512
 
@@ -75,8 +74,9 @@ struct DecodeParams {
 
 /* Routing inputs of the prep kernel. mode 0: idx/w are given; mode 1: raw
  * logits [M][n_experts] were written to `logits` by router_logits_kernel;
- * mode 2: the router GEMV runs inside prep. In modes 1 and 2 `logits`
- * receives the post-activation scores and idx/w the selection. */
+ * mode 3: the prep launch is n_rwg router workgroups followed by the prep
+ * workgroup (see decode_prep_kernel). In modes 1 and 3 `logits` receives
+ * the post-activation scores and idx/w the selection. */
 struct RouteArgs {
     const uint16_t* W;
     const uint16_t* bias;
@@ -84,6 +84,10 @@ struct RouteArgs {
     float* logits;
     int* idx;
     float* w;
+    int n_rwg;            /* mode 3: router workgroups of rpw rows each        */
+    int rpw;
+    uint32_t* epoch;      /* mode 3: calls completed on this workspace         */
+    uint64_t* words;      /* mode 3: [M][n_experts] (call token << 32 | logit) */
 };
 
 /* ======================================================================= */
@@ -92,18 +96,40 @@ struct RouteArgs {
 
 __host__ __device__ constexpr int align_up_dev(int v, int a) { return (v + a - 1) / a * a; }
 
-/* Dynamic LDS of the prep kernel in routing modes 1 and 2: 64-bit selection
- * keys, M rows of scores, and (mode 2) the M token rows. */
-static inline size_t prep_lds_bytes(int mode, int n_experts, int M, int hidden, size_t xsz) {
-    if (mode == 0) return 0;
-    return (size_t)align_up_dev(n_experts * 8, 16) + align_up_dev(M * n_experts * 4, 16) +
-           (mode == 2 ? (size_t)M * hidden * xsz : 0);
+/* LDS of the 64-bit selection keys: a multiple of 64, so each wave of the
+ * one-token selection ranks against 64 slots. */
+__host__ __device__ constexpr int prep_key_bytes(int n_experts) {
+    return align_up_dev(n_experts, 64) * 8;
 }
 
-/* One workgroup of DEC_PREP_THREADS. Every global load it needs (the expert
- * table, and in mode 2 each wave's first router row and the token rows) is
- * issued before the first barrier, so the kernel costs about one memory
- * round trip. */
+/* Dynamic LDS of the prep kernel in routing modes 1 and 3: selection keys
+ * and M rows of scores. */
+static inline size_t prep_lds_bytes(int mode, int n_experts, int M) {
+    if (mode == 0) return 0;
+    return (size_t)prep_key_bytes(n_experts) + align_up_dev(M * n_experts * 4, 16);
+}
+
+/* Polls of one routing word before the prep workgroup gives up on it (about
+ * 80 ms): the wait ends even if a router workgroup never ran. */
+#define DEC_POLL_LIMIT (1 << 16)
+
+/* The prep workgroup has DEC_PREP_THREADS threads.
+ *
+ * Mode 3 launches n_rwg + 1 workgroups. Router workgroup g computes the raw
+ * logits of rows
+ * [rpw g, rpw g + rpw) (rpw = 1 up to 256 experts, so the matrix is read by
+ * as many CUs as there are rows: one CU streams only a few tens of GB/s),
+ * its threads splitting the row into 16-byte pieces with the matching x
+ * elements loaded straight into registers, and publishes each logit as one
+ * 64-bit word (call token << 32 | float bits) with a device-coherent store.
+ * The last
+ * workgroup, the prep proper, polls those words until each carries this
+ * call's token, then selects as in mode 1. The token is epoch + 1, epoch a
+ * workspace word that the prep workgroup advances once it has seen every
+ * word (so every router workgroup has read epoch by then); a word is never
+ * reset, so no call needs the workspace zeroed. The prep workgroup is
+ * dispatched after the router workgroups, which wait on nothing, so its wait
+ * always ends; the poll bound is a second guarantee. */
 template <typename XT>
 __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     DecodeParams P, RouteArgs R, const void* const* __restrict__ table, const void* shared_blob,
@@ -114,9 +140,88 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     __shared__ int s_wcount[NWV];
     __shared__ const uint8_t* s_tab[DEC_ROUTE_MAX_EXPERTS];
     __shared__ float s_red[32];
+    __shared__ __attribute__((aligned(16))) uint64_t s_cand[64];
+    __shared__ int s_sel[DEC_MAX_TOPK];
     const int M = P.M;
     const int n_pairs = M * top_k;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+
+    if (R.mode == 3 && (int)blockIdx.x < R.n_rwg) {
+        /* router workgroup: rows [rpw g, rpw g + rpw), one after another;
+         * thread i takes the 16-byte weight pieces i and i + DEC_PREP_THREADS
+         * of a row and keeps the matching x elements as raw 16-byte pieces */
+        constexpr int RMAX = 4, PIECES = 2, XU = sizeof(XT) / 2;
+        __shared__ float s_part[NWV][RMAX * DEC_MAX_TOKENS];
+        const uint32_t tok =
+            __hip_atomic_load(R.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+        const int n8 = P.hidden / 8;
+        const int e0 = blockIdx.x * R.rpw;
+        const int nr = min(R.rpw, n_experts - e0);
+        u4 xr[DEC_MAX_TOKENS][PIECES][XU];
+        u4 wpc[PIECES];
+#pragma unroll
+        for (int j = 0; j < PIECES; j++) {
+            const int pc = min((int)threadIdx.x + j * DEC_PREP_THREADS, n8 - 1);
+            wpc[j] = ((const u4*)(R.W + (size_t)e0 * P.hidden))[pc];
+#pragma unroll
+            for (int t = 0; t < DEC_MAX_TOKENS; t++)
+#pragma unroll
+                for (int c = 0; c < XU; c++)
+                    if (t < M) xr[t][j][c] = ((const u4*)(x + (size_t)t * P.hidden + (size_t)pc * 8))[c];
+        }
+        for (int r = 0; r < nr; r++) {
+            if (r > 0) {
+#pragma unroll
+                for (int j = 0; j < PIECES; j++) {
+                    const int pc = min((int)threadIdx.x + j * DEC_PREP_THREADS, n8 - 1);
+                    wpc[j] = ((const u4*)(R.W + (size_t)(e0 + r) * P.hidden))[pc];
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < DEC_MAX_TOKENS; t++) {
+                if (t >= M) break;
+                float a = 0.0f;
+#pragma unroll
+                for (int j = 0; j < PIECES; j++) {
+                    const bool in = (int)threadIdx.x + j * DEC_PREP_THREADS < n8;
+                    const h8 wh = __builtin_bit_cast(h8, wpc[j]);
+                    float xv[8];
+                    if (XU == 1) {
+                        const h8 xh = __builtin_bit_cast(h8, xr[t][j][0]);
+#pragma unroll
+                        for (int q = 0; q < 8; q++) xv[q] = (float)xh[q];
+                    } else {
+                        const f4 lo = __builtin_bit_cast(f4, xr[t][j][0]);
+                        const f4 hi = __builtin_bit_cast(f4, xr[t][j][XU - 1]);
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            xv[q] = lo[q];
+                            xv[4 + q] = hi[q];
+                        }
+                    }
+#pragma unroll
+                    for (int q = 0; q < 8; q++)
+                        a = __builtin_fmaf((float)wh[q], in ? xv[q] : 0.0f, a);
+                }
+                a = wave_sum_dpp(a);
+                if (lane == 0) s_part[wv][r * DEC_MAX_TOKENS + t] = a;
+            }
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < nr * DEC_MAX_TOKENS) {
+            const int r = threadIdx.x / DEC_MAX_TOKENS, t = threadIdx.x % DEC_MAX_TOKENS;
+            if (t < M) {
+                float a = 0.0f;
+                for (int w = 0; w < NWV; w++) a += s_part[w][threadIdx.x];
+                const int e = e0 + r;
+                if (R.kind == WISP_ROUTER_SOFTMAX && R.bias) a += half_bits_to_float(R.bias[e]);
+                __hip_atomic_store(R.words + (size_t)t * n_experts + e,
+                                   ((uint64_t)tok << 32) | __float_as_uint(a), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        return;
+    }
 
     for (int e = threadIdx.x; e < n_experts; e += blockDim.x) s_tab[e] = (const uint8_t*)table[e];
     for (int i = threadIdx.x; i < P.hidden / 16; i += blockDim.x) P.tile_cnt[i] = 0;
@@ -127,30 +232,33 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     }
 
     if (R.mode != 0) {
-        /* dynamic LDS: 64-bit selection keys [n_experts] (scratch of the
-         * top-k), scores [M][n_experts] (the raw logits first), then x
-         * [M][hidden] (mode 2) */
+        /* dynamic LDS: 64-bit selection keys (scratch of the top-k), then
+         * scores [M][n_experts] (the raw logits first) */
         extern __shared__ __attribute__((aligned(16))) uint8_t lds_raw[];
         uint64_t* s_ck = (uint64_t*)lds_raw;
-        float* s_sc = (float*)(lds_raw + align_up_dev(n_experts * 8, 16));
+        float* s_sc = (float*)(lds_raw + prep_key_bytes(n_experts));
         if (R.mode == 1) {
             /* raw logits from router_logits_kernel, loaded with everything else */
             for (int i = threadIdx.x; i < M * n_experts; i += blockDim.x) s_sc[i] = R.logits[i];
             __syncthreads();
-        } else {
-            XT* s_x = (XT*)(lds_raw + align_up_dev(n_experts * 8, 16) +
-                            align_up_dev(M * n_experts * 4, 16));
-            u4 wrow[ROUTE_UNROLL];
-            if (wv < n_experts) router_row_load(R.W + (size_t)wv * P.hidden, P.hidden, lane, wrow);
-            stage_rows<XT>(s_x, x, M, P.hidden);
-            __syncthreads();
-            const uint16_t* bias = R.kind == WISP_ROUTER_SOFTMAX ? R.bias : nullptr;
-            for (int e = wv; e < n_experts; e += NWV) {
-                if (e != wv) router_row_load(R.W + (size_t)e * P.hidden, P.hidden, lane, wrow);
-                router_row_fma<XT>(wrow, s_x, M, P.hidden, lane, s_sc + e, n_experts,
-                                   bias ? half_bits_to_float(bias[e]) : 0.0f);
+        } else if (R.mode == 3) {
+            /* raw logits published by this launch's router workgroups */
+            const uint32_t tok =
+                __hip_atomic_load(R.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+            int polls = 0;
+            for (int i = threadIdx.x; i < M * n_experts; i += blockDim.x) {
+                uint64_t v = __hip_atomic_load(R.words + i, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                while ((uint32_t)(v >> 32) != tok && polls < DEC_POLL_LIMIT) {
+                    __builtin_amdgcn_s_sleep(8);
+                    polls++;
+                    v = __hip_atomic_load(R.words + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                s_sc[i] = __uint_as_float((uint32_t)v);
             }
             __syncthreads();
+            if (threadIdx.x == 0)
+                __hip_atomic_store(R.epoch, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         /* One token: the selection is distinct, so wave 0 writes it and the
          * unique list directly (shared expert first, then rank order). */
@@ -176,13 +284,19 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
             }
         };
         if (M == 1 && n_experts <= 64) {
-            /* few experts: wave 0 selects in registers, no further barrier */
+            /* few experts: wave 0 selects alone, no further barrier */
             if (wv != 0) return;
             int e;
             float w;
             topk_wave_small(s_sc, R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr, R.logits,
-                            n_experts, top_k, R.kind, e, w);
+                            s_ck, s_sel, n_experts, top_k, R.kind, e, w);
             one_token_list(e, w);
+            return;
+        }
+        if (M == 1 && n_experts <= 256 && top_k <= 16) {
+            /* one token, up to 256 experts: two-level selection, one barrier */
+            topk_one_token(s_sc, R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr, R.logits, s_ck,
+                           s_cand, s_sel, s_red, n_experts, top_k, R.kind, one_token_list);
             return;
         }
         for (int t = 0; t < M; t++)
@@ -786,7 +900,7 @@ static int dec_chunk_blocks(int nblk) {
 }
 
 struct WsLayout {
-    size_t nu, tile_cnt, ublob, uw, xconv, hperm, part, total;
+    size_t nu, epoch, tile_cnt, ublob, uw, xconv, hperm, part, rwords, total;
     int max_u;
 };
 
@@ -795,6 +909,7 @@ static WsLayout ws_layout(const WispExpertLayout* L, int M, int top_k, int has_s
     w.max_u = (has_shared ? 1 : 0) + M * top_k;
     size_t off = 0;
     w.nu = off; off += 256;
+    w.epoch = off; off += 256;
     w.tile_cnt = off; off = align_up(off + (size_t)(L->cols[0] / 16) * sizeof(int), 256);
     w.ublob = off; off = align_up(off + (size_t)w.max_u * sizeof(void*), 256);
     w.uw = off; off = align_up(off + (size_t)w.max_u * 4 * sizeof(float), 256);
@@ -803,6 +918,7 @@ static WsLayout ws_layout(const WispExpertLayout* L, int M, int top_k, int has_s
     const int nblk = (int)(L->rows[0] / 128);
     const size_t nch = (nblk + dec_chunk_blocks(nblk) - 1) / dec_chunk_blocks(nblk);
     w.part = off; off = align_up(off + (size_t)w.max_u * nch * M * L->cols[0] * 4, 256);
+    w.rwords = off; off = align_up(off + (size_t)M * DEC_ROUTE_MAX_EXPERTS * 8, 256);
     w.total = off;
     return w;
 }
@@ -916,15 +1032,25 @@ static hipError_t decode_run(const void* const* d_expert_table, const void* d_sh
     P.out16 = (uint16_t*)d_out_f16;
     P.accumulate = accumulate ? 1 : 0;
 
-    const size_t xsz = x_dtype == WISP_DTYPE_F16 ? 2 : 4;
-    const size_t lds = prep_lds_bytes(R.mode, n_experts, M, P.hidden, xsz);
+    const size_t lds = prep_lds_bytes(R.mode, n_experts, M);
+    int grid = 1;
+    if (R.mode == 3) {
+        R.rpw = (n_experts + 255) / 256;
+        R.n_rwg = (n_experts + R.rpw - 1) / R.rpw;
+        R.epoch = (uint32_t*)(ws + w.epoch);
+        R.words = (uint64_t*)(ws + w.rwords);
+        grid = R.n_rwg + 1;
+    }
     ev_before(EV_PREP, s);
+    /* dynamic LDS <= 8 KiB keys + 16 KiB scores (1024 experts, 4 tokens) */
     if (x_dtype == WISP_DTYPE_F16)
-        hipLaunchKernelGGL(decode_prep_kernel<uint16_t>, dim3(1), dim3(DEC_PREP_THREADS), lds, s, P, R,
-                           d_expert_table, d_shared_blob, (const uint16_t*)d_x, top_k, n_experts);
+        hipLaunchKernelGGL(decode_prep_kernel<uint16_t>, dim3(grid), dim3(DEC_PREP_THREADS), lds, s,
+                           P, R, d_expert_table, d_shared_blob, (const uint16_t*)d_x, top_k,
+                           n_experts);
     else
-        hipLaunchKernelGGL(decode_prep_kernel<float>, dim3(1), dim3(DEC_PREP_THREADS), lds, s, P, R,
-                           d_expert_table, d_shared_blob, (const float*)d_x, top_k, n_experts);
+        hipLaunchKernelGGL(decode_prep_kernel<float>, dim3(grid), dim3(DEC_PREP_THREADS), lds, s,
+                           P, R, d_expert_table, d_shared_blob, (const float*)d_x, top_k,
+                           n_experts);
     ev_after(EV_PREP, s);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -958,7 +1084,8 @@ extern "C" hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table
     if (!decode_args_ok(d_expert_table, d_x, x_dtype, n_tokens, top_k, n_experts, d_workspace,
                         d_out_f32, d_out_f16) || !d_topk_idx || !d_topk_w)
         return hipErrorInvalidValue;
-    RouteArgs R = {nullptr, nullptr, 0, 0, nullptr, (int*)d_topk_idx, (float*)d_topk_w};
+    RouteArgs R = {nullptr, nullptr, 0, 0, nullptr, (int*)d_topk_idx, (float*)d_topk_w,
+                   0, 0, nullptr, nullptr};
     return decode_run(d_expert_table, d_shared_blob, L, d_x, x_dtype, n_tokens, R, top_k,
                       n_experts, d_workspace, workspace_bytes, accumulate, d_out_f32, d_out_f16, s);
 }
@@ -983,15 +1110,17 @@ extern "C" hipError_t wisp_gpu_moe_layer_decode_int4(
         return hipErrorInvalidValue;
     if (wisp_expert_layout_check(L) != hipSuccess) return hipErrorInvalidValue;
     const int hidden = (int)L->cols[0];
-    const size_t xsz = x_dtype == WISP_DTYPE_F16 ? 2 : 4;
-    const size_t prep_lds = prep_lds_bytes(2, n_experts, n_tokens, hidden, xsz);
-    const bool fuse = (size_t)n_experts * hidden * 2 <= DEC_ROUTE_FUSE_BYTES &&
-                      hidden <= ROUTE_UNROLL * WAVE * 8 &&
-                      prep_lds <= 65536 && (uintptr_t)d_router_w % 16 == 0 &&
-                      (uintptr_t)d_x % 16 == 0;
+    /* the router GEMV runs in router workgroups of the prep launch (mode 3):
+     * each thread takes at most 2 16-byte pieces of a row, so rows up to
+     * 8192, and 16-byte aligned W and x; otherwise it gets a launch of its
+     * own (mode 1) */
+    const int mode = hidden <= 2 * DEC_PREP_THREADS * 8 && (uintptr_t)d_router_w % 16 == 0 &&
+                             (uintptr_t)d_x % 16 == 0
+                         ? 3
+                         : 1;
     RouteArgs R = {(const uint16_t*)d_router_w, (const uint16_t*)d_router_bias, router_kind,
-                   fuse ? 2 : 1, d_scores, d_topk_idx, d_topk_w};
-    if (!fuse) {
+                   mode, d_scores, d_topk_idx, d_topk_w, 0, 0, nullptr, nullptr};
+    if (mode == 1) {
         ev_before(EV_ROUTE, s);
         hipError_t e = wisp_amd__router_logits(d_router_w, d_router_bias, d_x, x_dtype, n_tokens,
                                                hidden, n_experts,

@@ -89,40 +89,103 @@ __device__ __forceinline__ void router_row_load(const uint16_t* __restrict__ row
     }
 }
 
-/* Lane 0 writes out[t * out_stride] = add + the dot of the loaded row with
- * token t's x row (x in LDS), for t < nt. Tokens are a runtime loop to keep
- * the code small. */
+/* DPP lane moves within rows of 16 lanes (gfx9 encodings). */
+#define DPP_QUAD_XOR1 0xB1   /* quad_perm [1,0,3,2] */
+#define DPP_QUAD_XOR2 0x4E   /* quad_perm [2,3,0,1] */
+#define DPP_ROW_ROR4 0x124
+#define DPP_ROW_ROR8 0x128
+
+#define DPP_MOVE(v, ctrl) \
+    __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), (ctrl), 0xF, 0xF, false))
+
+/* Sum over the 64 lanes, the same value in every lane. Order: quads (lane
+ * xor 1, xor 2), then within each row quad + quad rotated by 4, then by 8,
+ * then the four row totals (r0 + r1) + (r2 + r3). DPP moves and readlanes
+ * only: no LDS round trips. */
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += DPP_MOVE(v, DPP_QUAD_XOR1);
+    v += DPP_MOVE(v, DPP_QUAD_XOR2);
+    v += DPP_MOVE(v, DPP_ROW_ROR4);
+    v += DPP_MOVE(v, DPP_ROW_ROR8);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+/* Maximum over the 64 lanes (NaN-ignoring fmaxf), in every lane. */
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, DPP_MOVE(v, DPP_QUAD_XOR1));
+    v = fmaxf(v, DPP_MOVE(v, DPP_QUAD_XOR2));
+    v = fmaxf(v, DPP_MOVE(v, DPP_ROW_ROR4));
+    v = fmaxf(v, DPP_MOVE(v, DPP_ROW_ROR8));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+/* The dot of the loaded row with token t's x row (x in LDS), summed over
+ * the wave: every lane returns it. Branch-free: past the row end a lane's
+ * weights are zero (router_row_load) and its x operands are replaced by
+ * zeros, so every LDS read of the unrolled loop can be in flight at once. */
+template <typename XT>
+__device__ __forceinline__ float router_row_dot1(const u4 (&w)[ROUTE_UNROLL], const XT* x, int t,
+                                                 int hidden, int lane) {
+    const int n8 = hidden / 8;
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ROUTE_UNROLL; i++) {
+        const int c8 = i * WAVE + lane;
+        const bool in = c8 < n8;
+        const h8 wh = __builtin_bit_cast(h8, w[i]);
+        float xv[8];
+        load_x8(x + (size_t)t * hidden + (size_t)(in ? c8 : 0) * 8, xv);
+#pragma unroll
+        for (int e = 0; e < 8; e++) a = __builtin_fmaf((float)wh[e], in ? xv[e] : 0.0f, a);
+    }
+    return wave_sum_dpp(a);
+}
+
+/* Lane 0 writes out[t * out_stride] = add + router_row_dot1(t), for t < nt.
+ * Tokens are a runtime loop to keep the code small. */
 template <typename XT>
 __device__ __forceinline__ void router_row_fma(const u4 (&w)[ROUTE_UNROLL], const XT* x, int nt,
                                                int hidden, int lane, float* out, int out_stride,
                                                float add) {
-    const int n8 = hidden / 8;
 #pragma unroll 1
     for (int t = 0; t < nt; t++) {
-        float a = 0.0f;
-#pragma unroll
-        for (int i = 0; i < ROUTE_UNROLL; i++) {
-            const int c8 = i * WAVE + lane;
-            if (c8 < n8) {
-                const h8 wh = __builtin_bit_cast(h8, w[i]);
-                float xv[8];
-                load_x8(x + (size_t)t * hidden + (size_t)c8 * 8, xv);
-#pragma unroll
-                for (int e = 0; e < 8; e++) a = __builtin_fmaf((float)wh[e], xv[e], a);
-            }
-        }
-        a = wave_sum(a);
+        const float a = router_row_dot1<XT>(w, x, t, hidden, lane);
         if (lane == 0) out[(size_t)t * out_stride] = a + add;
     }
 }
 
 /* Copies nt rows of x [nt][hidden] (16-byte aligned, hidden % 8 == 0) to
- * LDS with 16-byte accesses, in the caller's type. */
+ * LDS with 16-byte accesses, in the caller's type. Up to 8 pieces per
+ * thread are loaded before any is stored, so the copy costs one memory round
+ * trip per 8 x blockDim pieces (a load-store loop would wait for each load,
+ * and its first wait also for every load the caller issued before). */
 template <typename XT>
 __device__ __forceinline__ void stage_rows(XT* dst, const XT* __restrict__ src, int nt, int hidden) {
     constexpr int PER16 = 16 / sizeof(XT);
+    constexpr int CAP = 8;
     const int n = nt * hidden / PER16;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) ((u4*)dst)[i] = ((const u4*)src)[i];
+    const int nthr = blockDim.x;
+    for (int base = 0; base < n; base += CAP * nthr) {
+        u4 v[CAP];
+#pragma unroll
+        for (int c = 0; c < CAP; c++) {
+            const int i = base + (int)threadIdx.x + c * nthr;
+            if (i < n) v[c] = ((const u4*)src)[i];
+        }
+#pragma unroll
+        for (int c = 0; c < CAP; c++) {
+            const int i = base + (int)threadIdx.x + c * nthr;
+            if (i < n) ((u4*)dst)[i] = v[c];
+        }
+    }
 }
 
 /* Selection key of expert e as one unsigned 64-bit number: the high word
@@ -145,15 +208,36 @@ __device__ __forceinline__ uint64_t readlane64(uint64_t v, int lane) {
     return ((uint64_t)hi << 32) | lo;
 }
 
+/* Rank of `ce` among the 2 NP keys at keys[0..2 NP) in LDS (16-byte
+ * aligned): the number of larger keys. Every lane reads the same 16 bytes
+ * at a time (a broadcast), all reads unrolled, so they are in flight
+ * together; a loop of v_readlane over the keys instead costs about a
+ * hundred cycles per key in its register dependencies. */
+template <int NP>
+__device__ __forceinline__ int lds_rank(const uint64_t* keys, uint64_t ce) {
+    const u64x2* k2 = (const u64x2*)keys;
+    int rank = 0;
+#pragma unroll
+    for (int q = 0; q < NP; q++) {
+        const u64x2 v = k2[q];
+        rank += (v.x > ce) + (v.y > ce);
+    }
+    return rank;
+}
+
 /* One wave, n_experts <= 64, one token: the selection topk_block makes,
- * with the same arithmetic in the same order (so the same bits), but
- * every reduction in registers: no LDS and no barrier. lg: the token's raw
- * logits (LDS or global). Writes scores_out[e]; lane q < top_k returns the
+ * with the same formulas, but no barrier: reductions in registers (DPP
+ * moves and readlanes), the rank against the wave's 64 keys in LDS, the
+ * selection placed by an LDS scatter. Weights and scores agree with
+ * topk_block's to rounding (sums run in another order). lg: the token's
+ * raw logits (LDS or global); s_key: 64 u64 of LDS (16-byte aligned);
+ * s_sel: top_k ints of LDS. Writes scores_out[e]; lane q < top_k returns the
  * q-th selection in sel_e (-1 past the candidates) and its renormalised
  * weight in sel_w. */
 __device__ __forceinline__ void topk_wave_small(const float* lg, const uint16_t* __restrict__ bias,
-                                                float* scores_out, int n_experts, int top_k,
-                                                int kind, int& sel_e, float& sel_w) {
+                                                float* scores_out, uint64_t* s_key, int* s_sel,
+                                                int n_experts, int top_k, int kind, int& sel_e,
+                                                float& sel_w) {
     const bool sig = kind == WISP_ROUTER_SIGMOID;
     const int lane = threadIdx.x & 63;
     const bool act = lane < n_experts;
@@ -161,33 +245,100 @@ __device__ __forceinline__ void topk_wave_small(const float* lg, const uint16_t*
     float key = l;
     if (act && sig && bias) key = 1.0f / (1.0f + __expf(-l)) + half_bits_to_float(bias[lane]);
     const uint64_t ce = act ? route_composite(key, lane) : 0ull;
-    float mx = l;
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, WAVE));
+    s_key[lane] = ce;
+    const float mx = wave_max_dpp(l);
     const float v = act ? (sig ? 1.0f / (1.0f + __expf(-l)) : __expf(l - mx)) : 0.0f;
-    const float denom = wave_sum(v);
+    const float denom = wave_sum_dpp(v);
     const float inv = 1.0f / (denom > 0.0f ? denom : 1.0f);
     const float score = sig ? v : v * inv;
     if (act) scores_out[lane] = score;
-    int rank = 0;
-    for (int j = 0; j < n_experts; j++) rank += readlane64(ce, j) > ce;
+    const int rank = lds_rank<32>(s_key, ce);
     const bool picked = act && (ce >> 32) != 0 && rank < top_k;
     /* lane q takes the expert of rank q */
-    sel_e = -1;
+    if (lane < top_k) s_sel[lane] = -1;
+    if (picked) s_sel[rank] = lane;
+    sel_e = lane < top_k ? s_sel[lane] : -1;
     sel_w = 0.0f;
-    for (int q = 0; q < top_k; q++) {
-        const uint64_t m = __ballot(picked && rank == q);
-        if (m) {
-            const int src = __builtin_ctzll(m);
-            const float sv = __shfl(score, src, WAVE);
-            if (lane == q) {
-                sel_e = src;
-                sel_w = sv;
+    if (sel_e >= 0) {
+        const float ls = lg[sel_e];
+        const float vs = sig ? 1.0f / (1.0f + __expf(-ls)) : __expf(ls - mx);
+        sel_w = sig ? vs : vs * inv;
+    }
+    const float wsum = wave_sum_dpp(sel_w);
+    if (wsum > 0.0f) sel_w /= wsum;
+}
+
+/* One token, 64 < n_experts <= 256, top_k <= 16, a workgroup of at least
+ * four waves. Waves 0-3 rank the keys of experts 64 w + lane against their
+ * own wave's 64 keys; a key in the global top_k is in its wave's top_k, so
+ * the keys of local rank < top_k are the candidates. After one barrier wave
+ * 0 ranks the 4 top_k candidates and calls emit(e, w) with lane q < top_k
+ * holding the q-th selection (-1 and 0 past the candidates); then every
+ * wave writes the scores of its experts, so no global store precedes the
+ * barrier or the emit. The selection is topk_block's; weights and scores use
+ * the same formulas, with the softmax denominator summed per wave (rescaled
+ * to the global maximum), so they agree to rounding. LDS: s_key 256 u64,
+ * s_cand 64 u64 (both 16-byte aligned), s_sel 16 ints, s_red 8 floats. */
+template <typename Emit>
+__device__ __forceinline__ void topk_one_token(const float* lg, const uint16_t* __restrict__ bias,
+                                               float* scores_out, uint64_t* s_key,
+                                               uint64_t* s_cand, int* s_sel, float* s_red,
+                                               int n_experts, int top_k, int kind, Emit emit) {
+    const bool sig = kind == WISP_ROUTER_SIGMOID;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int e = wv * 64 + lane;
+    const bool act = wv < 4 && e < n_experts;
+    const float l = act ? lg[e] : -INFINITY;
+    const float sg = sig ? 1.0f / (1.0f + __expf(-l)) : 0.0f;
+    const float key = (sig && bias && act) ? sg + half_bits_to_float(bias[e]) : (sig ? sg : l);
+    const uint64_t ce = act ? route_composite(key, e) : 0ull;
+    if (wv < 4) {
+        s_key[e] = ce;
+        const int rank = lds_rank<32>(s_key + wv * 64, ce);
+        if (lane < top_k) s_cand[wv * top_k + lane] = 0ull;
+        if (act && (ce >> 32) != 0 && rank < top_k) s_cand[wv * top_k + rank] = ce;
+        if (!sig) {
+            const float wmax = wave_max_dpp(l);
+            const float wsum = wave_sum_dpp(act ? __expf(l - wmax) : 0.0f);
+            if (lane == 0) {
+                s_red[wv] = wmax;
+                s_red[4 + wv] = wsum;
             }
         }
     }
-    float wsum = 0.0f;
-    for (int q = 0; q < top_k; q++) wsum += __shfl(sel_w, q, WAVE);
-    if (wsum > 0.0f) sel_w /= wsum;
+    __syncthreads();
+    if (wv >= 4) return;
+    float mx = 0.0f, inv = 1.0f;
+    if (!sig) {
+        mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+        float den = 0.0f;
+        for (int q = 0; q < 4; q++)
+            if (s_red[4 + q] != 0.0f) den += s_red[4 + q] * __expf(s_red[q] - mx);
+        inv = 1.0f / (den > 0.0f ? den : 1.0f);
+    }
+    if (wv == 0) {
+        const int nc = 4 * top_k;
+        const uint64_t cc = lane < nc ? s_cand[lane] : 0ull;
+        /* rank among the candidates: 4 top_k <= 64 keys, read in pairs */
+        const u64x2* c2 = (const u64x2*)s_cand;
+        int rank = 0;
+#pragma unroll 8
+        for (int q = 0; q < nc / 2; q++) {
+            const u64x2 v = c2[q];
+            rank += (v.x > cc) + (v.y > cc);
+        }
+        if (lane < top_k) s_sel[lane] = -1;
+        if (lane < nc && (cc >> 32) != 0 && rank < top_k) s_sel[rank] = (int)~(uint32_t)cc;
+        const int sel_e = lane < top_k ? s_sel[lane] : -1;
+        float v = 0.0f;
+        if (sel_e >= 0) {
+            const float ls = lg[sel_e];
+            v = sig ? 1.0f / (1.0f + __expf(-ls)) : __expf(ls - mx) * inv;
+        }
+        const float wsum = wave_sum_dpp(v);
+        emit(sel_e, wsum > 0.0f ? v / wsum : v);
+    }
+    if (act) scores_out[e] = sig ? sg : __expf(l - mx) * inv;
 }
 
 /* All threads of the workgroup, one token. lg: the token's raw logits
