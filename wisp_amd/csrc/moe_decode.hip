@@ -27,13 +27,16 @@
  *             reduced through LDS in a fixed order; the epilogue writes
  *             h' = w_route * silu(g) * u in fp16, already permuted for the
  *             down kernel.
- *   down    : grid (hidden/16 row tiles) x (unique experts x K chunks of at
- *             most 4096). Each workgroup computes its partial sums (routing
- *             weights are already folded into h'); the last workgroup of a
- *             row tile to arrive adds the tile's partials in a fixed order
- *             (shared expert, then routed experts in unique-list order, then
- *             K chunk) and writes the output, so the result is
- *             deterministic. The hand-off uses device-coherent stores and
+ *   down    : the K axes of the unique experts' down matrices, concatenated
+ *             in unique-list order, form one axis cut into wave units of 8
+ *             blocks of 128 (units never straddle experts); grid (hidden/16
+ *             row tiles) x (chunks of 4 units). Each wave stages its own
+ *             unit's h' and scales in its own LDS region, so nothing waits
+ *             for another wave before the dot products; each workgroup writes
+ *             its partial sums (routing weights are already folded into h');
+ *             the last workgroup of a row tile to arrive adds the tile's
+ *             partials in chunk order and writes the output, so the result
+ *             is deterministic. The hand-off uses device-coherent stores and
  *             loads of the partials plus an arrival counter, not a fence: a
  *             device-scope fence writes back the whole L2 on this part, far
  *             more costly than the few partials involved.
@@ -46,7 +49,8 @@
 #define DEC_MAX_TOKENS 4
 #define DEC_MAX_TOPK 64
 #define DEC_MAX_WAVES 8
-#define DEC_CHUNK_MAX 32      /* down-projection K chunk per workgroup: at most 32 blocks of 128 */
+#define DEC_UNIT_BLOCKS 8     /* down projection: 128-wide K blocks per wave unit */
+#define DN_WAVES 4            /* down projection: wave units per workgroup */
 #define DEC_ROUTE_MAX_EXPERTS 1024
 #define DEC_PREP_THREADS 512
 
@@ -54,8 +58,8 @@ struct DecodeParams {
     uint64_t p_off[3], s_off[3], z_off[3];
     int hidden, inter, gs, has_zeros;
     int gshift;           /* log2(gs * NG / 128): block -> group index */
-    int n_chunks;         /* down-projection K chunks of chunk_blocks 128-wide blocks */
-    int chunk_blocks;     /* a multiple of 8 (one wave per 8 blocks), see dec_chunk_blocks */
+    int upe;              /* down projection: wave units per expert, ceil(inter / 1024) */
+    int n_q_max;          /* down projection: workgroups per row tile at max_u experts */
     uint32_t m_lo, m_hi, one024;  /* unpack masks 0x000F000F, 0x00F000F0, 0x64006400 */
     int max_u;
     int M;
@@ -64,8 +68,8 @@ struct DecodeParams {
     float* uw;            /* [max_u][4] routing weight of each token     */
     const uint16_t* xh;   /* [M][hidden] fp16 activations (caller's or a converted copy) */
     uint16_t* xconv;      /* workspace copy used when the caller's x is fp32 or unaligned */
-    uint16_t* hperm;      /* [max_u][M][inter] permuted fp16 h'           */
-    float* part;          /* [max_u][n_chunks][M][hidden] down partials   */
+    uint16_t* hperm;      /* [M][max_u * inter] permuted fp16 h'          */
+    float* part;          /* [n_q_max][M][hidden] down partials           */
     int* tile_cnt;        /* [hidden / 16] down workgroups arrived per row tile */
     float* out32;         /* [M][hidden] layer output (either may be null) */
     uint16_t* out16;
@@ -447,19 +451,6 @@ __host__ __device__ inline LdsMap lds_map(int M, int NT, int xk, int gs_count, b
     return L;
 }
 
-/* Copies M activation rows (K range [k0, k0 + xk) of rows of length K) into
- * the LDS x image with 16-byte accesses. */
-template <int M>
-__device__ __forceinline__ void stage_x(uint8_t* smem, const LdsMap& L, const uint16_t* src, int K,
-                                        int k0, int xk) {
-    uint16_t* xs = (uint16_t*)(smem + L.x_off);
-    const int per_row = xk / 8;
-    for (int i = threadIdx.x; i < M * per_row; i += blockDim.x) {
-        const int v = i / per_row, c = i - v * per_row;
-        *(u4*)(xs + v * L.XR + c * 8) = *(const u4*)(src + (size_t)v * K + k0 + c * 8);
-    }
-}
-
 /* Copies the raw scale (or zero) bits of 16 consecutive rows starting at
  * row r0 of a [rows][G] fp16 table, groups [g0, g0 + gn), into dst[16][gn]. */
 __device__ __forceinline__ void stage_groups(uint16_t* dst, const uint16_t* tab, int G, int r0,
@@ -702,7 +693,7 @@ __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void gateup_kernel(const Decode
         const int r = r0 + 16 * q + c;
         const int e = r & 7;
         f16 hv = (f16)((e & 1) ? h * 0.0625f : h);
-        P.hperm[((size_t)u * M + v) * P.inter + (r & ~7) + perm_slot(e)] =
+        P.hperm[((size_t)v * P.max_u + u) * P.inter + (r & ~7) + perm_slot(e)] =
             __builtin_bit_cast(uint16_t, hv);
     }
 }
@@ -720,141 +711,168 @@ __device__ __forceinline__ void store_out(const DecodeParams& P, size_t i, float
     if (P.out16) P.out16[i] = __builtin_bit_cast(uint16_t, (f16)y);
 }
 
-/* grid (hidden / (16 TILES), max_u * n_chunks): workgroup (row tile,
- * unique expert u, K chunk c of chunk_blocks blocks) computes
- * part[u][c][v][row] = down_u[row, chunk] . h'_u[v][chunk] (routing weight
- * already folded into h'). The last of the row tile's n_unique * n_chunks
- * workgroups to arrive adds all of the tile's partials in a fixed order
- * (shared expert, then routed experts in unique-list order, then K chunk)
- * and writes the output, so the result is deterministic. The hand-off needs
- * no cache write-back: partials are stored and loaded with device-coherent
- * accesses, every store is acknowledged before the arrival is counted, and
- * the counters are zeroed by the prep kernel of the same call. */
-template <int M, int NG, int TILES, int NB, bool HZ>
-__global__ __launch_bounds__(64 * DEC_MAX_WAVES) void down_kernel(const DecodeParams P) {
-    constexpr int NT = TILES;
+/* LDS image of one down wave: x [M][1024 + 32] (its unit's h', rows padded
+ * so tokens fall in different banks), sc [16][GMAX] and zc [16][GMAX] raw
+ * fp16 scale and zero bits of the tile's rows for the unit's groups. */
+__host__ __device__ inline LdsMap down_wave_map(int M, int gmax, bool hz, int wave) {
+    LdsMap L;
+    L.XR = DEC_UNIT_BLOCKS * 128 + 32;
+    L.GS = gmax;
+    int bytes = M * L.XR * 2;
+    bytes = (bytes + 15) & ~15;
+    const int sc = bytes;
+    bytes += 16 * gmax * 2;
+    bytes = (bytes + 15) & ~15;
+    const int zc = bytes;
+    if (hz) bytes += 16 * gmax * 2;
+    bytes = (bytes + 15) & ~15;
+    L.x_off = wave * bytes;
+    L.sc_off = L.x_off + sc;
+    L.zc_off = L.x_off + zc;
+    L.red_off = DN_WAVES * bytes;
+    L.bytes = L.red_off + DN_WAVES * 16 * M * 4;
+    return L;
+}
+
+/* grid (hidden / 16, n_q_max): workgroup (row tile rt, chunk q) covers wave
+ * units [DN_WAVES q, DN_WAVES q + DN_WAVES) of the concatenated K axis and
+ * computes part[q][v][row] = sum over its units of down_u[row, unit] .
+ * h'_u[v][unit] (routing weight already folded into h'). The last of the row
+ * tile's n_q workgroups to arrive adds all of the tile's partials in chunk
+ * order and writes the output, so the result is deterministic. The hand-off
+ * needs no cache write-back: partials are stored and loaded with
+ * device-coherent accesses, every store is acknowledged before the arrival
+ * is counted, and the counters are zeroed by the prep kernel of the same
+ * call. */
+template <int M, int NG, bool HZ>
+__global__ __launch_bounds__(64 * DN_WAVES) void down_kernel(const DecodeParams P) {
+    constexpr int NB = DEC_UNIT_BLOCKS;
+    constexpr int GMAX = NB * NG;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ int s_last;
-    const int nch = P.n_chunks;
-    const int u = blockIdx.y / nch, c = blockIdx.y - u * nch;
-    const int r0 = blockIdx.x * 16 * TILES;
+    const int rt = blockIdx.x, q = blockIdx.y;
+    const int r0 = rt * 16;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, j = lane >> 4;
+    const int K = P.inter, H = P.hidden;
+    const int nblk = K >> 7;
+    const int gu = q * DN_WAVES + wave;
+    const int u = min(gu / P.upe, P.max_u - 1);
+    /* both loads in one round trip */
     const int n_u = *P.n_unique;
     const uint8_t* blob = P.ublob[u];
-    if (u >= n_u) {
+    const int n_units = n_u * P.upe;
+    const int n_q = (n_units + DN_WAVES - 1) / DN_WAVES;
+    if (q >= n_q) {
         /* nothing routed: one workgroup per row tile writes the empty sum */
-        if (n_u == 0 && blockIdx.y == 0)
-            for (int o = threadIdx.x; o < TILES * 16 * M; o += blockDim.x)
-                store_out(P, (size_t)(o / (16 * TILES)) * P.hidden + r0 + o % (16 * TILES), 0.0f);
+        if (n_u == 0 && q == 0)
+            for (int o = threadIdx.x; o < 16 * M; o += blockDim.x)
+                store_out(P, (size_t)(o / 16) * H + r0 + o % 16, 0.0f);
         return;
     }
-    const int K = P.inter, H = P.hidden;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    const int col = lane & 15, j = lane >> 4;
-    const int nblk = K >> 7;
+    /* a wave past the last unit (its slot u may hold no blob) loads nothing */
+    const bool live = gu < n_units;
+    const int lb0 = live ? (gu - u * P.upe) * NB : 0;
+    const int lb1 = live ? min(lb0 + NB, nblk) : 0;
+    const int nb = lb1 - lb0;
     const int G = K / P.gs;
-    const int cb0 = c * P.chunk_blocks, cb1 = min(cb0 + P.chunk_blocks, nblk);
-    const int g_lo = (cb0 * NG) >> P.gshift, g_hi = (((cb1 * NG) - 1) >> P.gshift) + 1;
-    const int nb = cb1 - cb0;
-    /* wave w owns blocks [cb0 + NB w, cb0 + NB w + NB) of the chunk */
-    const int b0 = cb0 + wave * NB, b1 = min(b0 + NB, cb1);
-    const LdsMap L = lds_map(M, NT, P.chunk_blocks * 128, g_hi - g_lo, HZ, nw);
+    const int g_lo = (lb0 * NG) >> P.gshift;
+    const int gn = nb > 0 ? ((((lb1 * NG) - 1) >> P.gshift) + 1 - g_lo) : 0;
+    const LdsMap L = down_wave_map(M, GMAX, HZ, wave);
 
-    const uint8_t* wp[NT];
+    float tot[1][M];
 #pragma unroll
-    for (int s = 0; s < NT; s++)
-        wp[s] = blob + P.p_off[2] + (size_t)(r0 + 16 * s + col) * (K / 2) + 16 * j;
-    /* Same order as the gate/up kernel: h' chunk and scales, then weights.
-     * A row's scales of the chunk are (g_hi - g_lo) * 2 bytes at a row
-     * stride of 2 G bytes; 16-byte pieces need both to be multiples of 16
-     * (always true for a single chunk: then the 16 rows are contiguous). */
-    constexpr int XCNT = M * NB / 4 > 0 ? M * NB / 4 : 1;
-    constexpr int SCNT = NB * NG / 16 > 0 ? NB * NG / 16 : 1;
-    const int gn = g_hi - g_lo;
-    const bool one_run = nch == 1;
-    const int s_rows = one_run ? 1 : 16;
-    const int s_w16 = one_run ? 2 * G : gn / 8;
-    const bool fast = Stage16<XCNT>::ok(M, nb * 16) && Stage16<SCNT>::ok(s_rows, s_w16) &&
-                      (one_run || (G % 8 == 0 && g_lo % 8 == 0 && gn % 8 == 0));
-    Stage16<XCNT> sx;
-    Stage16<SCNT> ssc[NT], szc[NT];
-    if (fast) {
-        sx.issue((const uint8_t*)(P.hperm + (size_t)u * M * K + cb0 * 128), (size_t)K * 2, M,
-                 nb * 16);
+    for (int v = 0; v < M; v++) tot[0][v] = 0.0f;
+    if (live) {
+    /* order of issue: the unit's h' and scales, then its weights (loads
+     * return in order, so the LDS writes wait only for the former) */
+    u4 xv[M][2];
+    const uint16_t* hsrc = P.hperm + (size_t)u * K + lb0 * 128;
 #pragma unroll
-        for (int s = 0; s < NT; s++) {
-            const size_t roff = ((size_t)(r0 + 16 * s) * G + g_lo) * 2;
-            ssc[s].issue(blob + P.s_off[2] + roff, (size_t)G * 2, s_rows, s_w16);
-            if (HZ) szc[s].issue(blob + P.z_off[2] + roff, (size_t)G * 2, s_rows, s_w16);
+    for (int v = 0; v < M; v++)
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int i = min(lane + 64 * c, nb * 16 - 1);
+            xv[v][c] = *(const u4*)(hsrc + (size_t)v * P.max_u * K + i * 8);
+        }
+    constexpr int SCNT = (16 * GMAX + 63) / 64;
+    uint16_t sv[SCNT], zv[SCNT];
+    const uint16_t* stab = (const uint16_t*)(blob + P.s_off[2]);
+    const uint16_t* ztab = (const uint16_t*)(blob + P.z_off[2]);
+#pragma unroll
+    for (int c = 0; c < SCNT; c++) {
+        const int i = lane + 64 * c;
+        const int ii = min(i, 16 * gn - 1);
+        const int rr = ii / gn, gg = ii - rr * gn;
+        const size_t at = (size_t)(r0 + rr) * G + g_lo + gg;
+        sv[c] = stab[at];
+        zv[c] = HZ ? ztab[at] : (uint16_t)0;
+    }
+    const uint8_t* wp[1] = {blob + P.p_off[2] + (size_t)(r0 + col) * (K / 2) + 16 * j};
+    u4 w[NB][1];
+    load_blocks<1, NB>(wp, lb0, lb1 - 1, w);
+
+    uint16_t* xs = (uint16_t*)(smem + L.x_off);
+#pragma unroll
+    for (int v = 0; v < M; v++)
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int i = lane + 64 * c;
+            if (i < nb * 16) *(u4*)(xs + v * L.XR + i * 8) = xv[v][c];
+        }
+    uint16_t* ss = (uint16_t*)(smem + L.sc_off);
+    uint16_t* zs = (uint16_t*)(smem + L.zc_off);
+#pragma unroll
+    for (int c = 0; c < SCNT; c++) {
+        const int i = lane + 64 * c;
+        if (i < 16 * gn) {
+            const int rr = i / gn, gg = i - rr * gn;
+            ss[rr * GMAX + gg] = sv[c];
+            if (HZ) zs[rr * GMAX + gg] = zv[c];
         }
     }
-    u4 w[NB][NT];
-    load_blocks<NT, NB>(wp, b0, cb1 - 1, w);
-    if (fast) {
-        sx.template commit<false>(smem + L.x_off, L.XR * 2);
-#pragma unroll
-        for (int s = 0; s < NT; s++) {
-            ssc[s].template commit<false>(smem + L.sc_off + s * 32 * L.GS, L.GS * 2);
-            if (HZ) szc[s].template commit<false>(smem + L.zc_off + s * 32 * L.GS, L.GS * 2);
-        }
-    } else {
-        stage_x<M>(smem, L, P.hperm + (size_t)u * M * K, K, cb0 * 128, nb * 128);
-#pragma unroll
-        for (int s = 0; s < NT; s++) {
-            stage_groups((uint16_t*)(smem + L.sc_off) + s * 16 * L.GS,
-                         (const uint16_t*)(blob + P.s_off[2]), G, r0 + 16 * s, g_lo, L.GS);
-            if (HZ)
-                stage_groups((uint16_t*)(smem + L.zc_off) + s * 16 * L.GS,
-                             (const uint16_t*)(blob + P.z_off[2]), G, r0 + 16 * s, g_lo, L.GS);
-        }
+    /* the wave reads only its own region: LDS operations of one wave run in
+     * order, so no barrier; keep the compiler from hoisting the reads */
+    __builtin_amdgcn_wave_barrier();
+    compute_blocks<M, NG, 1, NB, HZ>(w, smem, L, lb0, lb1, lb0, g_lo, P.gshift, col, j,
+                                     P.m_lo, P.m_hi, P.one024, tot);
     }
-    __syncthreads();
-
-    float tot[NT][M];
-#pragma unroll
-    for (int s = 0; s < NT; s++)
-#pragma unroll
-        for (int v = 0; v < M; v++) tot[s][v] = 0.0f;
-    compute_blocks<M, NG, NT, NB, HZ>(w, smem, L, b0, b1, cb0, g_lo, P.gshift, col, j, P.m_lo,
-                                      P.m_hi, P.one024, tot);
 
     float* red = (float*)(smem + L.red_off);
     if (lane < 16) {
 #pragma unroll
-        for (int s = 0; s < NT; s++)
-#pragma unroll
-            for (int v = 0; v < M; v++) red[((wave * NT + s) * 16 + col) * M + v] = tot[s][v];
+        for (int v = 0; v < M; v++) red[(wave * 16 + col) * M + v] = tot[0][v];
     }
     __syncthreads();
-    for (int o = threadIdx.x; o < TILES * 16 * M; o += blockDim.x) {
-        const int v = o % M, rc = o / M, q = rc / 16, cc = rc % 16;
+    for (int o = threadIdx.x; o < 16 * M; o += blockDim.x) {
+        const int v = o % M, cc = o / M;
         float y = 0.0f;
-        for (int ww = 0; ww < nw; ww++) y += red[((ww * NT + q) * 16 + cc) * M + v];
-        __hip_atomic_store(P.part + (((size_t)u * nch + c) * M + v) * H + r0 + 16 * q + cc, y,
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int ww = 0; ww < DN_WAVES; ww++) y += red[(ww * 16 + cc) * M + v];
+        __hip_atomic_store(P.part + ((size_t)q * M + v) * H + r0 + cc, y, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
     __builtin_amdgcn_s_waitcnt(0);   /* this thread's partial stores are acknowledged */
     __syncthreads();
-    const int n_q = n_u * nch;
     if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(P.tile_cnt + blockIdx.x, 1, __ATOMIC_RELAXED,
+        s_last = __hip_atomic_fetch_add(P.tile_cnt + rt, 1, __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT) == n_q - 1;
     __syncthreads();
     if (!s_last) return;
     constexpr int MAXQ = 16;
-    for (int o = threadIdx.x; o < TILES * 16 * M; o += blockDim.x) {
-        const int v = o / (16 * TILES), r = r0 + o % (16 * TILES);
+    for (int o = threadIdx.x; o < 16 * M; o += blockDim.x) {
+        const int v = o / 16, r = r0 + o % 16;
         const float* src = P.part + (size_t)v * H + r;
         const size_t stride = (size_t)M * H;
         float y = 0.0f;
         for (int q0 = 0; q0 < n_q; q0 += MAXQ) {
             float t[MAXQ];
 #pragma unroll
-            for (int q = 0; q < MAXQ; q++)
-                t[q] = q0 + q < n_q ? __hip_atomic_load(src + (size_t)(q0 + q) * stride,
-                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                    : 0.0f;
+            for (int qq = 0; qq < MAXQ; qq++)
+                t[qq] = q0 + qq < n_q ? __hip_atomic_load(src + (size_t)(q0 + qq) * stride,
+                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                      : 0.0f;
 #pragma unroll
-            for (int q = 0; q < MAXQ; q++) y += t[q];
+            for (int qq = 0; qq < MAXQ; qq++) y += t[qq];
         }
         store_out(P, (size_t)v * H + r, y);
     }
@@ -889,19 +907,9 @@ extern "C" hipError_t wisp_expert_layout_check(const WispExpertLayout* L) {
     return hipSuccess;
 }
 
-/* Down-projection K chunk: the fewest chunks of at most DEC_CHUNK_MAX
- * blocks, as even as a multiple of 8 blocks (one wave each) allows
- * (Mixtral inter 14336: 32, 32, 32, 16 blocks; measured faster on MI355X
- * than 2 chunks of 56 blocks at 7 waves). */
-static int dec_chunk_blocks(int nblk) {
-    const int nch = (nblk + DEC_CHUNK_MAX - 1) / DEC_CHUNK_MAX;
-    const int c = (nblk + nch - 1) / nch;
-    return (c + 7) / 8 * 8;
-}
-
 struct WsLayout {
     size_t nu, epoch, tile_cnt, ublob, uw, xconv, hperm, part, rwords, total;
-    int max_u;
+    int max_u, n_q_max;
 };
 
 static WsLayout ws_layout(const WispExpertLayout* L, int M, int top_k, int has_shared) {
@@ -915,9 +923,9 @@ static WsLayout ws_layout(const WispExpertLayout* L, int M, int top_k, int has_s
     w.uw = off; off = align_up(off + (size_t)w.max_u * 4 * sizeof(float), 256);
     w.xconv = off; off = align_up(off + (size_t)M * L->cols[0] * 2, 256);
     w.hperm = off; off = align_up(off + (size_t)w.max_u * M * L->rows[0] * 2, 256);
-    const int nblk = (int)(L->rows[0] / 128);
-    const size_t nch = (nblk + dec_chunk_blocks(nblk) - 1) / dec_chunk_blocks(nblk);
-    w.part = off; off = align_up(off + (size_t)w.max_u * nch * M * L->cols[0] * 4, 256);
+    const int upe = (int)((L->rows[0] / 128 + DEC_UNIT_BLOCKS - 1) / DEC_UNIT_BLOCKS);
+    w.n_q_max = (w.max_u * upe + DN_WAVES - 1) / DN_WAVES;
+    w.part = off; off = align_up(off + (size_t)w.n_q_max * M * L->cols[0] * 4, 256);
     w.rwords = off; off = align_up(off + (size_t)M * DEC_ROUTE_MAX_EXPERTS * 8, 256);
     w.total = off;
     return w;
@@ -944,19 +952,11 @@ static void launch_gateup(const DecodeParams& P, hipStream_t s) {
     hipLaunchKernelGGL(k, dim3(P.inter / (16 * TILES), P.max_u), dim3(64 * waves), L.bytes, s, P);
 }
 
-template <int M, int NG, int TILES, int NB, bool HZ>
+template <int M, int NG, bool HZ>
 static void launch_down(const DecodeParams& P, hipStream_t s) {
-    const int nblk = P.inter / 128;
-    const int chunk = nblk < P.chunk_blocks ? nblk : P.chunk_blocks;
-    const int waves = (chunk + NB - 1) / NB;
-    /* LDS sized for the largest chunk and its groups */
-    const int ng_hi = (((P.chunk_blocks * NG) - 1) >> P.gshift) + 2;
-    const LdsMap L = lds_map(M, TILES, P.chunk_blocks * 128, ng_hi, HZ, waves);
-    auto k = down_kernel<M, NG, TILES, NB, HZ>;
-    if (L.bytes > 65536)
-        (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, L.bytes);
-    hipLaunchKernelGGL(k, dim3(P.hidden / (16 * TILES), P.max_u * P.n_chunks), dim3(64 * waves),
-                       L.bytes, s, P);
+    const LdsMap L = down_wave_map(M, DEC_UNIT_BLOCKS * NG, HZ, 0);
+    auto k = down_kernel<M, NG, HZ>;
+    hipLaunchKernelGGL(k, dim3(P.hidden / 16, P.n_q_max), dim3(64 * DN_WAVES), L.bytes, s, P);
 }
 
 template <int M, int NG, bool HZ>
@@ -966,7 +966,7 @@ static void launch_compute(const DecodeParams& P, hipStream_t s) {
     else launch_gateup<M, NG, 1, 8, HZ>(P, s);
     ev_after(EV_GATEUP, s);
     ev_before(EV_DOWN, s);
-    launch_down<M, NG, 1, 8, HZ>(P, s);
+    launch_down<M, NG, HZ>(P, s);
     ev_after(EV_DOWN, s);
 }
 
@@ -1011,8 +1011,8 @@ static hipError_t decode_run(const void* const* d_expert_table, const void* d_sh
         while ((128 << sh) < ngs) sh++;
         P.gshift = sh;
     }
-    P.chunk_blocks = dec_chunk_blocks(P.inter / 128);
-    P.n_chunks = (P.inter / 128 + P.chunk_blocks - 1) / P.chunk_blocks;
+    P.upe = (P.inter / 128 + DEC_UNIT_BLOCKS - 1) / DEC_UNIT_BLOCKS;
+    P.n_q_max = w.n_q_max;
     P.m_lo = 0x000F000Fu;
     P.m_hi = 0x00F000F0u;
     P.one024 = 0x64006400u;
