@@ -106,6 +106,11 @@ class Layer:
                                   self.xptr(i), self.M, s.top_k, s.n_experts, self.ws,
                                   self.out32.ptr, self.out16.ptr, self.stream.handle)
 
+    def fused_experts(self):
+        """True when gate/up and down run in one launch: one token and at
+        most 4 gate/up waves (hidden <= 4096); otherwise two launches."""
+        return self.M == 1 and self.shape.hidden <= 4096
+
     def separate_router(self):
         """True when the router GEMV gets its own launch: only for rows longer
         than 8192 (otherwise it runs in router workgroups of the prep launch)."""
@@ -113,8 +118,9 @@ class Layer:
 
     def token_bytes(self):
         """Per pool token: algorithmic HBM bytes (packed + scales; zeros are
-        +0 and not read) of the gate/up kernel, the down kernel, the router
-        and the layer, from the routing the device produces for it."""
+        +0 and not read) of the expert kernel (gate, up and down of every
+        unique expert), the router and the layer, from the routing the
+        device produces for it."""
         from wisp_amd.hip import synchronize
         if self._bytes is None:
             s = self.shape
@@ -126,7 +132,7 @@ class Layer:
                 synchronize()
                 ids = self.idx.download(np.int32, (self.M, s.top_k))
                 n_u = len({int(e) for e in ids.reshape(-1)}) + (1 if s.shared else 0)
-                out.append({"n_unique": n_u, "gate_up": 2 * n_u * mat, "down": n_u * mat,
+                out.append({"n_unique": n_u, "experts": 3 * n_u * mat,
                             "router": router, "layer": 3 * n_u * mat + router})
             self._bytes = out
         return self._bytes
@@ -174,13 +180,20 @@ def time_layer(layer, steps, warmup):
         layer.step(i)
     lib.wisp_amd_set_kernel_events(None, 0)
     synchronize()
+    def kernel_us(k):
+        return 1e3 * float(np.mean([evs[i][2 * k].elapsed_ms(evs[i][2 * k + 1])
+                                    for i in range(steps)]))
+
     kern = {}
-    kinds = (("prep", EV_PREP), ("gate_up", EV_GATEUP), ("down", EV_DOWN))
     if layer.separate_router():
-        kinds = (("router_gemv", EV_ROUTE),) + kinds
-    for name, k in kinds:
-        kern[name] = 1e3 * float(np.mean([evs[i][2 * k].elapsed_ms(evs[i][2 * k + 1])
-                                          for i in range(steps)]))
+        kern["router_gemv"] = kernel_us(EV_ROUTE)
+    kern["prep"] = kernel_us(EV_PREP)
+    if layer.fused_experts():
+        kern["experts"] = kernel_us(EV_GATEUP)
+    else:
+        kern["gate_up"] = kernel_us(EV_GATEUP)
+        kern["down"] = kernel_us(EV_DOWN)
+        kern["experts"] = kern["gate_up"] + kern["down"]
     return {"us_per_layer": 1e3 * dev_ms / steps, "eager_us_per_layer": 1e3 * eager_ms / steps,
             "host_us_per_layer": 1e3 * host_ms / steps, "kernel_us": kern}
 
@@ -255,9 +268,8 @@ def measure(layer, steps, warmup):
         "layer_hbm_frac": round(b["layer"] / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "n_unique_experts": round(b["n_unique"], 2),
         "kernel_us": {k: round(v, 3) for k, v in r["kernel_us"].items()},
-        "gate_up": {**roofline(b["gate_up"], r["kernel_us"]["gate_up"]),
-                    "bytes_per_launch": int(b["gate_up"])},
-        "down": {**roofline(b["down"], r["kernel_us"]["down"]), "bytes_per_launch": int(b["down"])},
+        "experts": {**roofline(b["experts"], r["kernel_us"]["experts"]),
+                    "bytes_per_launch": int(b["experts"])},
     }
 
 
@@ -490,8 +502,8 @@ def main():
     head = Layer(synth.MIXTRAL, 1, seed=1234, n_sets=4)
     m = measure(head, args.steps, args.warmup)
     log(f"mixtral M=1: {m['us_per_layer']:.2f} us/layer, kernels {m['kernel_us']}")
-    gu = dict(m["gate_up"])
-    gu["traffic"] = load_traffic("mixtral-decode-m1/gate_up")
+    gu = dict(m["experts"])
+    gu["traffic"] = load_traffic("mixtral-decode-m1/experts")
     result = {
         "metric": "us per MoE layer, int4 expert decode (Mixtral-8x7B shape, M=1)",
         "value": m["us_per_layer"],
@@ -513,9 +525,8 @@ def main():
         "kernel_us": m["kernel_us"],
         "roofline": {"bound": gu["bound"], "achieved": gu["achieved"], "peak": gu["peak"],
                      "unit": gu["unit"], "frac": gu["frac"], "traffic": gu["traffic"],
-                     "kernel": "moe gate_up (fused int4 gate+up+SiLU)",
+                     "kernel": "moe experts (int4 gate+up+SiLU and down in one launch)",
                      "bytes_per_launch": gu["bytes_per_launch"]},
-        "down_roofline": m["down"],
     }
     if not args.no_cpu:
         log("cpu baseline ...")

@@ -76,6 +76,16 @@ __device__ __forceinline__ f4 mfma16x16x32(h8 a, h8 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+/* The global-address-space view of a pointer. Pointers read from memory
+ * (an expert table, a blob's sections) are generic to the compiler, so loads
+ * through them become FLAT loads, which also count in lgkmcnt: every wait
+ * for a scalar load or LDS access then waits for all of them too. Loads
+ * through this view are global loads, counted in vmcnt only. */
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gptr(const T* p) {
+    return (const __attribute__((address_space(1))) T*)p;
+}
+
 __device__ __forceinline__ float silu_f(float g) {
     return g / (1.0f + __expf(-g));
 }

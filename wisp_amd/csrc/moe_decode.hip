@@ -41,6 +41,10 @@
  *             device-scope fence writes back the whole L2 on this part, far
  *             more costly than the few partials involved.
  *
+ * For one token and hidden <= 4096 the gate/up and down workgroups share one
+ * launch (expert_kernel): down waves wait on per-unit counters of the gate/up
+ * workgroups earlier in the grid.
+ *
  * Weights are read once, in place, from the reference blob layout
  * (csrc/core/wisp_engine.h:214-238); nothing is dequantised to memory.
  */
@@ -51,6 +55,8 @@
 #define DEC_MAX_WAVES 8
 #define DEC_UNIT_BLOCKS 8     /* down projection: 128-wide K blocks per wave unit */
 #define DN_WAVES 4            /* down projection: wave units per workgroup */
+#define DEC_HCNT_STRIDE 64    /* ints between wave-unit counters (own memory line each) */
+#define DEC_POLL_SLEEP 16     /* s_sleep units (64 cycles) between polls of a counter */
 #define DEC_ROUTE_MAX_EXPERTS 1024
 #define DEC_PREP_THREADS 512
 
@@ -71,6 +77,7 @@ struct DecodeParams {
     uint16_t* hperm;      /* [M][max_u * inter] permuted fp16 h'          */
     float* part;          /* [n_q_max][M][hidden] down partials           */
     int* tile_cnt;        /* [hidden / 16] down workgroups arrived per row tile */
+    int* hcnt;            /* [max_u * upe] gate/up workgroups done per wave unit (fused launch) */
     float* out32;         /* [M][hidden] layer output (either may be null) */
     uint16_t* out16;
     int accumulate;
@@ -100,10 +107,16 @@ struct RouteArgs {
 
 __host__ __device__ constexpr int align_up_dev(int v, int a) { return (v + a - 1) / a * a; }
 
-/* LDS of the 64-bit selection keys: a multiple of 64, so each wave of the
- * one-token selection ranks against 64 slots. */
+/* Slots of one key array: at least 256 (the grouped selection gives each of
+ * its four waves 64) and n_experts for the workgroup selection. */
+__host__ __device__ constexpr int prep_key_slots(int n_experts) {
+    return n_experts > 256 ? align_up_dev(n_experts, 64) : 256;
+}
+
+/* LDS of the 64-bit selection keys: two arrays, one per wave group of the
+ * grouped selection. */
 __host__ __device__ constexpr int prep_key_bytes(int n_experts) {
-    return align_up_dev(n_experts, 64) * 8;
+    return 2 * prep_key_slots(n_experts) * 8;
 }
 
 /* Dynamic LDS of the prep kernel in routing modes 1 and 3: selection keys
@@ -144,8 +157,8 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     __shared__ int s_wcount[NWV];
     __shared__ const uint8_t* s_tab[DEC_ROUTE_MAX_EXPERTS];
     __shared__ float s_red[32];
-    __shared__ __attribute__((aligned(16))) uint64_t s_cand[64];
-    __shared__ int s_sel[DEC_MAX_TOPK];
+    __shared__ __attribute__((aligned(16))) uint64_t s_cand[2][64];
+    __shared__ int s_sel[2][DEC_MAX_TOPK];
     const int M = P.M;
     const int n_pairs = M * top_k;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -229,6 +242,7 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
 
     for (int e = threadIdx.x; e < n_experts; e += blockDim.x) s_tab[e] = (const uint8_t*)table[e];
     for (int i = threadIdx.x; i < P.hidden / 16; i += blockDim.x) P.tile_cnt[i] = 0;
+    for (int i = threadIdx.x; i < P.max_u * P.upe; i += blockDim.x) P.hcnt[i * DEC_HCNT_STRIDE] = 0;
     /* x -> fp16 copy when the gate/up kernel cannot read the caller's x */
     if (P.xconv) {
         for (int i = threadIdx.x; i < M * P.hidden; i += blockDim.x)
@@ -293,24 +307,46 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
             int e;
             float w;
             topk_wave_small(s_sc, R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr, R.logits,
-                            s_ck, s_sel, n_experts, top_k, R.kind, e, w);
+                            s_ck, s_sel[0], n_experts, top_k, R.kind, e, w);
             one_token_list(e, w);
             return;
         }
-        if (M == 1 && n_experts <= 256 && top_k <= 16) {
-            /* one token, up to 256 experts: two-level selection, one barrier */
-            topk_one_token(s_sc, R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr, R.logits, s_ck,
-                           s_cand, s_sel, s_red, n_experts, top_k, R.kind, one_token_list);
-            return;
-        }
-        for (int t = 0; t < M; t++)
-            topk_block(s_sc + t * n_experts, R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr, s_ck,
-                       s_sc + t * n_experts, s_red, R.logits + (size_t)t * n_experts, n_experts,
-                       top_k, R.kind, s_e + t * top_k, s_w + t * top_k);
-        if (M == 1) {
-            if (wv != 0) return;
-            one_token_list(lane < top_k ? s_e[lane] : -1, lane < top_k ? s_w[lane] : 0.0f);
-            return;
+        if (n_experts <= 256 && top_k <= 16) {
+            /* up to 256 experts: two-level selection by groups of four
+             * waves, two tokens per pass, one barrier per pass */
+            const int grp = wv >> 2;
+            const int ka = prep_key_slots(n_experts);
+            const uint16_t* sbias = R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr;
+            if (M == 1) {
+                topk_one_token(s_sc, sbias, R.logits, s_ck, s_cand[0], s_sel[0], s_red,
+                               n_experts, top_k, R.kind, grp == 0 ? (wv & 3) : -1,
+                               one_token_list);
+                return;
+            }
+            for (int t0 = 0; t0 < M; t0 += NWV / 4) {
+                const int t = t0 + grp;
+                const int tt = t < M ? t : 0;
+                auto to_lds = [&](int e, float w) {
+                    if (lane < top_k) {
+                        s_e[t * top_k + lane] = e;
+                        s_w[t * top_k + lane] = w;
+                    }
+                };
+                topk_one_token(s_sc + tt * n_experts, sbias, R.logits + (size_t)tt * n_experts,
+                               s_ck + grp * ka, s_cand[grp], s_sel[grp], s_red + 8 * grp,
+                               n_experts, top_k, R.kind, t < M ? (wv & 3) : -1, to_lds);
+                __syncthreads();   /* the next pass reuses the groups' scratch */
+            }
+        } else {
+            for (int t = 0; t < M; t++)
+                topk_block(s_sc + t * n_experts, R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr,
+                           s_ck, s_sc + t * n_experts, s_red, R.logits + (size_t)t * n_experts,
+                           n_experts, top_k, R.kind, s_e + t * top_k, s_w + t * top_k);
+            if (M == 1) {
+                if (wv != 0) return;
+                one_token_list(lane < top_k ? s_e[lane] : -1, lane < top_k ? s_w[lane] : 0.0f);
+                return;
+            }
         }
     } else {
         for (int p = threadIdx.x; p < n_pairs; p += blockDim.x) {
@@ -457,7 +493,7 @@ __device__ __forceinline__ void stage_groups(uint16_t* dst, const uint16_t* tab,
                                              int g0, int gn) {
     for (int i = threadIdx.x; i < 16 * gn; i += blockDim.x) {
         const int r = i / gn, g = i - r * gn;
-        dst[i] = tab[(size_t)(r0 + r) * G + g0 + g];
+        dst[i] = gptr(tab)[(size_t)(r0 + r) * G + g0 + g];
     }
 }
 
@@ -485,7 +521,7 @@ struct Stage16 {
         for (int c = 0; c < CNT; c++) {
             const int i = min((int)threadIdx.x + c * (int)blockDim.x, total - 1);
             const int r = i / w16, q = i - r * w16;
-            v[c] = *(const u4*)(src + r * src_stride + 16 * q);
+            v[c] = *gptr((const u4*)(src + r * src_stride + 16 * q));
         }
     }
     /* perm: permute each piece (8 fp16) into unpack8_magic slot order with
@@ -526,7 +562,7 @@ __device__ __forceinline__ void load_blocks(const uint8_t* const (&wp)[NT], int 
     for (int p = 0; p < NB; p++) {
         const int bb = min(b_first + p, b_clamp);
 #pragma unroll
-        for (int s = 0; s < NT; s++) w[p][s] = *(const u4*)(wp[s] + (size_t)bb * 64);
+        for (int s = 0; s < NT; s++) w[p][s] = *gptr((const u4*)(wp[s] + (size_t)bb * 64));
     }
 }
 
@@ -596,13 +632,14 @@ __device__ __forceinline__ void stage_x_perm(uint8_t* smem, const LdsMap& L,
 /* gate/up + SiLU                                                           */
 /* ======================================================================= */
 
-/* grid (inter / (16 TILES), max_u); workgroup = TILES gate + TILES up row
- * tiles of unique expert blockIdx.y over the full hidden K, waves split K. */
-template <int M, int NG, int TILES, int NB, bool HZ>
-__global__ __launch_bounds__(64 * DEC_MAX_WAVES) void gateup_kernel(const DecodeParams P) {
+/* One gate/up workgroup: TILES gate + TILES up row tiles starting at row
+ * 16 TILES rt of unique expert u over the full hidden K, waves split K. In
+ * the fused launch (FUSED) h' is written with device-coherent stores and,
+ * once they are acknowledged, the workgroup counts itself on its wave
+ * unit's counter (the down waves of the same launch poll it). */
+template <int M, int NG, int TILES, int NB, bool HZ, bool FUSED>
+__device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt, uint8_t* smem) {
     constexpr int NT = 2 * TILES;
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const int u = blockIdx.y;
     /* both loads in one round trip (slot u < max_u always exists) */
     const int n_u = *P.n_unique;
     const uint8_t* blob = P.ublob[u];
@@ -610,7 +647,7 @@ __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void gateup_kernel(const Decode
     const int K = P.hidden;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int col = lane & 15, j = lane >> 4;
-    const int r0 = blockIdx.x * 16 * TILES;
+    const int r0 = rt * 16 * TILES;
     const int nblk = K >> 7;
     const int G = K / P.gs;
     /* wave w owns blocks [NB w, NB w + NB); the host launches ceil(nblk/NB) waves */
@@ -693,9 +730,27 @@ __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void gateup_kernel(const Decode
         const int r = r0 + 16 * q + c;
         const int e = r & 7;
         f16 hv = (f16)((e & 1) ? h * 0.0625f : h);
-        P.hperm[((size_t)v * P.max_u + u) * P.inter + (r & ~7) + perm_slot(e)] =
-            __builtin_bit_cast(uint16_t, hv);
+        uint16_t* dst = P.hperm + ((size_t)v * P.max_u + u) * P.inter + (r & ~7) + perm_slot(e);
+        if (FUSED)
+            __hip_atomic_store(dst, __builtin_bit_cast(uint16_t, hv), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        else
+            *dst = __builtin_bit_cast(uint16_t, hv);
     }
+    if (FUSED) {
+        __builtin_amdgcn_s_waitcnt(0);   /* this thread's h' stores are acknowledged */
+        __syncthreads();
+        if (threadIdx.x == 0)
+            __hip_atomic_fetch_add(P.hcnt + (u * P.upe + r0 / (DEC_UNIT_BLOCKS * 128)) * DEC_HCNT_STRIDE, 1,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+/* grid (inter / (16 TILES), max_u): gate/up of unique expert blockIdx.y. */
+template <int M, int NG, int TILES, int NB, bool HZ>
+__global__ __launch_bounds__(64 * DEC_MAX_WAVES) void gateup_kernel(const DecodeParams P) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    gateup_tile<M, NG, TILES, NB, HZ, false>(P, blockIdx.y, blockIdx.x, smem);
 }
 
 /* ======================================================================= */
@@ -714,7 +769,7 @@ __device__ __forceinline__ void store_out(const DecodeParams& P, size_t i, float
 /* LDS image of one down wave: x [M][1024 + 32] (its unit's h', rows padded
  * so tokens fall in different banks), sc [16][GMAX] and zc [16][GMAX] raw
  * fp16 scale and zero bits of the tile's rows for the unit's groups. */
-__host__ __device__ inline LdsMap down_wave_map(int M, int gmax, bool hz, int wave) {
+__host__ __device__ inline LdsMap down_wave_map(int M, int gmax, bool hz, int wave, int nw) {
     LdsMap L;
     L.XR = DEC_UNIT_BLOCKS * 128 + 32;
     L.GS = gmax;
@@ -729,13 +784,13 @@ __host__ __device__ inline LdsMap down_wave_map(int M, int gmax, bool hz, int wa
     L.x_off = wave * bytes;
     L.sc_off = L.x_off + sc;
     L.zc_off = L.x_off + zc;
-    L.red_off = DN_WAVES * bytes;
-    L.bytes = L.red_off + DN_WAVES * 16 * M * 4;
+    L.red_off = nw * bytes;
+    L.bytes = L.red_off + nw * 16 * M * 4;
     return L;
 }
 
-/* grid (hidden / 16, n_q_max): workgroup (row tile rt, chunk q) covers wave
- * units [DN_WAVES q, DN_WAVES q + DN_WAVES) of the concatenated K axis and
+/* Workgroup (row tile rt, chunk q) of nw waves covers wave units
+ * [nw q, nw q + nw) of the concatenated K axis and
  * computes part[q][v][row] = sum over its units of down_u[row, unit] .
  * h'_u[v][unit] (routing weight already folded into h'). The last of the row
  * tile's n_q workgroups to arrive adds all of the tile's partials in chunk
@@ -743,26 +798,27 @@ __host__ __device__ inline LdsMap down_wave_map(int M, int gmax, bool hz, int wa
  * needs no cache write-back: partials are stored and loaded with
  * device-coherent accesses, every store is acknowledged before the arrival
  * is counted, and the counters are zeroed by the prep kernel of the same
- * call. */
-template <int M, int NG, bool HZ>
-__global__ __launch_bounds__(64 * DN_WAVES) void down_kernel(const DecodeParams P) {
+ * call. In the fused launch (FUSED) each wave first waits until every
+ * gate/up workgroup of its unit has counted itself (a bounded poll: those
+ * workgroups come earlier in the grid and wait on nothing), then reads h'
+ * with device-coherent loads. */
+template <int M, int NG, bool HZ, bool FUSED>
+__device__ __forceinline__ void down_tile(const DecodeParams& P, int q, int rt, uint8_t* smem) {
     constexpr int NB = DEC_UNIT_BLOCKS;
     constexpr int GMAX = NB * NG;
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ int s_last;
-    const int rt = blockIdx.x, q = blockIdx.y;
     const int r0 = rt * 16;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int col = lane & 15, j = lane >> 4;
     const int K = P.inter, H = P.hidden;
     const int nblk = K >> 7;
-    const int gu = q * DN_WAVES + wave;
+    const int gu = q * nw + wave;
     const int u = min(gu / P.upe, P.max_u - 1);
     /* both loads in one round trip */
     const int n_u = *P.n_unique;
     const uint8_t* blob = P.ublob[u];
     const int n_units = n_u * P.upe;
-    const int n_q = (n_units + DN_WAVES - 1) / DN_WAVES;
+    const int n_q = (n_units + nw - 1) / nw;
     if (q >= n_q) {
         /* nothing routed: one workgroup per row tile writes the empty sum */
         if (n_u == 0 && q == 0)
@@ -778,23 +834,44 @@ __global__ __launch_bounds__(64 * DN_WAVES) void down_kernel(const DecodeParams 
     const int G = K / P.gs;
     const int g_lo = (lb0 * NG) >> P.gshift;
     const int gn = nb > 0 ? ((((lb1 * NG) - 1) >> P.gshift) + 1 - g_lo) : 0;
-    const LdsMap L = down_wave_map(M, GMAX, HZ, wave);
+    const LdsMap L = down_wave_map(M, GMAX, HZ, wave, nw);
 
     float tot[1][M];
 #pragma unroll
     for (int v = 0; v < M; v++) tot[0][v] = 0.0f;
     if (live) {
-    /* order of issue: the unit's h' and scales, then its weights (loads
-     * return in order, so the LDS writes wait only for the former) */
+    /* Order of issue (loads return in order). Alone: the unit's h' and
+     * scales, then its weights, so the LDS writes wait only for the former.
+     * Fused: the first poll of the unit's counter, the scales and the
+     * weights, then the wait for the counter (its load returns first), then
+     * h' (after the poll, so it sees every gate/up store): the poll's round
+     * trip overlaps the weight stream instead of preceding it. */
+    int hc = 0;
+    if (FUSED)
+        hc = __hip_atomic_load(P.hcnt + gu * DEC_HCNT_STRIDE, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     u4 xv[M][2];
     const uint16_t* hsrc = P.hperm + (size_t)u * K + lb0 * 128;
+    auto load_h = [&]() {
 #pragma unroll
-    for (int v = 0; v < M; v++)
+        for (int v = 0; v < M; v++)
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-            const int i = min(lane + 64 * c, nb * 16 - 1);
-            xv[v][c] = *(const u4*)(hsrc + (size_t)v * P.max_u * K + i * 8);
-        }
+            for (int c = 0; c < 2; c++) {
+                const int i = min(lane + 64 * c, nb * 16 - 1);
+                const uint16_t* src = hsrc + (size_t)v * P.max_u * K + i * 8;
+                if (FUSED) {
+                    const uint64_t a = __hip_atomic_load((const uint64_t*)src, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+                    const uint64_t b = __hip_atomic_load((const uint64_t*)src + 1,
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    xv[v][c] = (u4){(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b,
+                                    (uint32_t)(b >> 32)};
+                } else {
+                    xv[v][c] = *(const u4*)src;
+                }
+            }
+    };
+    if (!FUSED) load_h();
     constexpr int SCNT = (16 * GMAX + 63) / 64;
     uint16_t sv[SCNT], zv[SCNT];
     const uint16_t* stab = (const uint16_t*)(blob + P.s_off[2]);
@@ -805,12 +882,23 @@ __global__ __launch_bounds__(64 * DN_WAVES) void down_kernel(const DecodeParams 
         const int ii = min(i, 16 * gn - 1);
         const int rr = ii / gn, gg = ii - rr * gn;
         const size_t at = (size_t)(r0 + rr) * G + g_lo + gg;
-        sv[c] = stab[at];
-        zv[c] = HZ ? ztab[at] : (uint16_t)0;
+        sv[c] = gptr(stab)[at];
+        zv[c] = HZ ? gptr(ztab)[at] : (uint16_t)0;
     }
     const uint8_t* wp[1] = {blob + P.p_off[2] + (size_t)(r0 + col) * (K / 2) + 16 * j};
     u4 w[NB][1];
     load_blocks<1, NB>(wp, lb0, lb1 - 1, w);
+    if (FUSED) {
+        /* h' of this unit: written by nb * 8 gate/up workgroups */
+        int polls = 0;
+        while (hc < nb * 8 && polls < DEC_POLL_LIMIT) {
+            __builtin_amdgcn_s_sleep(DEC_POLL_SLEEP);
+            polls++;
+            hc = __hip_atomic_load(P.hcnt + gu * DEC_HCNT_STRIDE, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+        load_h();
+    }
 
     uint16_t* xs = (uint16_t*)(smem + L.x_off);
 #pragma unroll
@@ -847,7 +935,7 @@ __global__ __launch_bounds__(64 * DN_WAVES) void down_kernel(const DecodeParams 
     for (int o = threadIdx.x; o < 16 * M; o += blockDim.x) {
         const int v = o % M, cc = o / M;
         float y = 0.0f;
-        for (int ww = 0; ww < DN_WAVES; ww++) y += red[(ww * 16 + cc) * M + v];
+        for (int ww = 0; ww < nw; ww++) y += red[(ww * 16 + cc) * M + v];
         __hip_atomic_store(P.part + ((size_t)q * M + v) * H + r0 + cc, y, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -875,6 +963,33 @@ __global__ __launch_bounds__(64 * DN_WAVES) void down_kernel(const DecodeParams 
             for (int qq = 0; qq < MAXQ; qq++) y += t[qq];
         }
         store_out(P, (size_t)v * H + r, y);
+    }
+}
+
+/* grid (hidden / 16, n_q_max), DN_WAVES waves: the down projection alone. */
+template <int M, int NG, bool HZ>
+__global__ __launch_bounds__(64 * DN_WAVES) void down_kernel(const DecodeParams P) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    down_tile<M, NG, HZ, false>(P, blockIdx.y, blockIdx.x, smem);
+}
+
+/* One launch for gate/up and down: the first max_u * inter / 16 workgroups
+ * are gate/up workgroups (expert-major, so an expert's h' completes early),
+ * the rest down workgroups (chunk-major); a workgroup has as many waves as
+ * gate/up needs, which is also the down chunk's unit count. Down waves wait
+ * only on workgroups earlier in the grid, which wait on nothing, so every
+ * wait ends. */
+template <int M, int NG, int NB, bool HZ>
+__global__ __launch_bounds__(64 * DEC_MAX_WAVES) void expert_kernel(const DecodeParams P) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int n_rt = P.inter / 16;
+    const int n_gu = P.max_u * n_rt;
+    const int b = blockIdx.x;
+    if (b < n_gu) {
+        gateup_tile<M, NG, 1, NB, HZ, true>(P, b / n_rt, b % n_rt, smem);
+    } else {
+        const int d = b - n_gu, n_ro = P.hidden / 16;
+        down_tile<M, NG, HZ, true>(P, d / n_ro, d % n_ro, smem);
     }
 }
 
@@ -908,7 +1023,7 @@ extern "C" hipError_t wisp_expert_layout_check(const WispExpertLayout* L) {
 }
 
 struct WsLayout {
-    size_t nu, epoch, tile_cnt, ublob, uw, xconv, hperm, part, rwords, total;
+    size_t nu, epoch, tile_cnt, hcnt, ublob, uw, xconv, hperm, part, rwords, total;
     int max_u, n_q_max;
 };
 
@@ -924,8 +1039,10 @@ static WsLayout ws_layout(const WispExpertLayout* L, int M, int top_k, int has_s
     w.xconv = off; off = align_up(off + (size_t)M * L->cols[0] * 2, 256);
     w.hperm = off; off = align_up(off + (size_t)w.max_u * M * L->rows[0] * 2, 256);
     const int upe = (int)((L->rows[0] / 128 + DEC_UNIT_BLOCKS - 1) / DEC_UNIT_BLOCKS);
-    w.n_q_max = (w.max_u * upe + DN_WAVES - 1) / DN_WAVES;
+    /* partials: at most one chunk per wave unit (a one-wave workgroup) */
+    w.n_q_max = w.max_u * upe;
     w.part = off; off = align_up(off + (size_t)w.n_q_max * M * L->cols[0] * 4, 256);
+    w.hcnt = off; off = align_up(off + (size_t)w.max_u * upe * DEC_HCNT_STRIDE * sizeof(int), 256);
     w.rwords = off; off = align_up(off + (size_t)M * DEC_ROUTE_MAX_EXPERTS * 8, 256);
     w.total = off;
     return w;
@@ -953,16 +1070,48 @@ static void launch_gateup(const DecodeParams& P, hipStream_t s) {
 }
 
 template <int M, int NG, bool HZ>
-static void launch_down(const DecodeParams& P, hipStream_t s) {
-    const LdsMap L = down_wave_map(M, DEC_UNIT_BLOCKS * NG, HZ, 0);
+static void launch_down(DecodeParams P, hipStream_t s) {
+    P.n_q_max = (P.max_u * P.upe + DN_WAVES - 1) / DN_WAVES;
+    const LdsMap L = down_wave_map(M, DEC_UNIT_BLOCKS * NG, HZ, 0, DN_WAVES);
     auto k = down_kernel<M, NG, HZ>;
     hipLaunchKernelGGL(k, dim3(P.hidden / 16, P.n_q_max), dim3(64 * DN_WAVES), L.bytes, s, P);
 }
 
+/* gate/up and down in one launch (expert_kernel) */
+template <int M, int NG, int NB, bool HZ>
+static void launch_fused(DecodeParams P, hipStream_t s) {
+    const int waves = (P.hidden / 128 + NB - 1) / NB;
+    P.n_q_max = (P.max_u * P.upe + waves - 1) / waves;
+    const LdsMap Lg = lds_map(M, 2, P.hidden, P.hidden / P.gs, HZ, waves);
+    const LdsMap Ld = down_wave_map(M, DEC_UNIT_BLOCKS * NG, HZ, 0, waves);
+    const int lds = Lg.bytes > Ld.bytes ? Lg.bytes : Ld.bytes;
+    auto k = expert_kernel<M, NG, NB, HZ>;
+    if (lds > 65536)
+        (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    const int grid = P.max_u * (P.inter / 16) + P.n_q_max * (P.hidden / 16);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(64 * waves), lds, s, P);
+}
+
+/* One launch for gate/up and down when the gate/up workgroup leaves the
+ * down role its occupancy: one token and at most 4 waves (hidden <= 4096).
+ * The fused kernel takes the larger register budget and wave count of the
+ * two roles; with more tokens (more registers) or more waves (DeepSeek-V3's
+ * 7) its down waves ran at half the occupancy of the down kernel alone and
+ * the layer got slower (DeepSeek-V3 M=4: 281.6 against 224.7 us). */
 template <int M, int NG, bool HZ>
 static void launch_compute(const DecodeParams& P, hipStream_t s) {
+    const int nbw = blocks_per_wave(P.hidden / 128);
+    const int waves = (P.hidden / 128 + nbw - 1) / nbw;
+    if constexpr (M == 1) {
+        if (waves <= 4) {
+            ev_before(EV_GATEUP, s);
+            launch_fused<M, NG, 8, HZ>(P, s);
+            ev_after(EV_GATEUP, s);
+            return;
+        }
+    }
     ev_before(EV_GATEUP, s);
-    if (blocks_per_wave(P.hidden / 128) == 16) launch_gateup<M, NG, 1, 16, HZ>(P, s);
+    if (nbw == 16) launch_gateup<M, NG, 1, 16, HZ>(P, s);
     else launch_gateup<M, NG, 1, 8, HZ>(P, s);
     ev_after(EV_GATEUP, s);
     ev_before(EV_DOWN, s);
@@ -1012,7 +1161,7 @@ static hipError_t decode_run(const void* const* d_expert_table, const void* d_sh
         P.gshift = sh;
     }
     P.upe = (P.inter / 128 + DEC_UNIT_BLOCKS - 1) / DEC_UNIT_BLOCKS;
-    P.n_q_max = w.n_q_max;
+    P.n_q_max = w.n_q_max;   /* set per launch shape in launch_compute */
     P.m_lo = 0x000F000Fu;
     P.m_hi = 0x00F000F0u;
     P.one024 = 0x64006400u;
@@ -1021,6 +1170,7 @@ static hipError_t decode_run(const void* const* d_expert_table, const void* d_sh
     char* ws = (char*)d_workspace;
     P.n_unique = (int*)(ws + w.nu);
     P.tile_cnt = (int*)(ws + w.tile_cnt);
+    P.hcnt = (int*)(ws + w.hcnt);
     P.ublob = (const uint8_t**)(ws + w.ublob);
     P.uw = (float*)(ws + w.uw);
     const bool x_direct = x_dtype == WISP_DTYPE_F16 && ((uintptr_t)d_x % 16) == 0;

@@ -268,46 +268,51 @@ __device__ __forceinline__ void topk_wave_small(const float* lg, const uint16_t*
     if (wsum > 0.0f) sel_w /= wsum;
 }
 
-/* One token, 64 < n_experts <= 256, top_k <= 16, a workgroup of at least
- * four waves. Waves 0-3 rank the keys of experts 64 w + lane against their
- * own wave's 64 keys; a key in the global top_k is in its wave's top_k, so
- * the keys of local rank < top_k are the candidates. After one barrier wave
- * 0 ranks the 4 top_k candidates and calls emit(e, w) with lane q < top_k
- * holding the q-th selection (-1 and 0 past the candidates); then every
- * wave writes the scores of its experts, so no global store precedes the
+/* One token's selection by a group of four waves (wl = this wave's index in
+ * the group, or -1 for a wave outside every active group), n_experts <=
+ * 256, top_k <= 16. Waves wl = 0-3 rank the keys of experts 64 wl + lane
+ * against their own wave's 64 keys; a key in the global top_k is in its
+ * wave's top_k, so the keys of local rank < top_k are the candidates. After
+ * one barrier (every wave of the workgroup must call this together) wave
+ * wl = 0 ranks the 4 top_k candidates and calls emit(e, w) with lane q <
+ * top_k holding the q-th selection (-1 and 0 past the candidates); then the
+ * group writes the scores of its experts, so no global store precedes the
  * barrier or the emit. The selection is topk_block's; weights and scores use
  * the same formulas, with the softmax denominator summed per wave (rescaled
- * to the global maximum), so they agree to rounding. LDS: s_key 256 u64,
- * s_cand 64 u64 (both 16-byte aligned), s_sel 16 ints, s_red 8 floats. */
+ * to the global maximum), so they agree to rounding. Group LDS: s_key 256
+ * u64, s_cand 64 u64 (both 16-byte aligned), s_sel 16 ints, s_red 8
+ * floats. */
 template <typename Emit>
 __device__ __forceinline__ void topk_one_token(const float* lg, const uint16_t* __restrict__ bias,
                                                float* scores_out, uint64_t* s_key,
                                                uint64_t* s_cand, int* s_sel, float* s_red,
-                                               int n_experts, int top_k, int kind, Emit emit) {
+                                               int n_experts, int top_k, int kind, int wl,
+                                               Emit emit) {
     const bool sig = kind == WISP_ROUTER_SIGMOID;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int e = wv * 64 + lane;
-    const bool act = wv < 4 && e < n_experts;
+    const int lane = threadIdx.x & 63;
+    const bool grp = wl >= 0 && wl < 4;
+    const int e = (grp ? wl : 0) * 64 + lane;
+    const bool act = grp && e < n_experts;
     const float l = act ? lg[e] : -INFINITY;
     const float sg = sig ? 1.0f / (1.0f + __expf(-l)) : 0.0f;
     const float key = (sig && bias && act) ? sg + half_bits_to_float(bias[e]) : (sig ? sg : l);
     const uint64_t ce = act ? route_composite(key, e) : 0ull;
-    if (wv < 4) {
+    if (grp) {
         s_key[e] = ce;
-        const int rank = lds_rank<32>(s_key + wv * 64, ce);
-        if (lane < top_k) s_cand[wv * top_k + lane] = 0ull;
-        if (act && (ce >> 32) != 0 && rank < top_k) s_cand[wv * top_k + rank] = ce;
+        const int rank = lds_rank<32>(s_key + wl * 64, ce);
+        if (lane < top_k) s_cand[wl * top_k + lane] = 0ull;
+        if (act && (ce >> 32) != 0 && rank < top_k) s_cand[wl * top_k + rank] = ce;
         if (!sig) {
             const float wmax = wave_max_dpp(l);
             const float wsum = wave_sum_dpp(act ? __expf(l - wmax) : 0.0f);
             if (lane == 0) {
-                s_red[wv] = wmax;
-                s_red[4 + wv] = wsum;
+                s_red[wl] = wmax;
+                s_red[4 + wl] = wsum;
             }
         }
     }
     __syncthreads();
-    if (wv >= 4) return;
+    if (!grp) return;
     float mx = 0.0f, inv = 1.0f;
     if (!sig) {
         mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
@@ -316,7 +321,7 @@ __device__ __forceinline__ void topk_one_token(const float* lg, const uint16_t* 
             if (s_red[4 + q] != 0.0f) den += s_red[4 + q] * __expf(s_red[q] - mx);
         inv = 1.0f / (den > 0.0f ? den : 1.0f);
     }
-    if (wv == 0) {
+    if (wl == 0) {
         const int nc = 4 * top_k;
         const uint64_t cc = lane < nc ? s_cand[lane] : 0ull;
         /* rank among the candidates: 4 top_k <= 64 keys, read in pairs */
