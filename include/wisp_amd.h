@@ -193,13 +193,14 @@ hipError_t wisp_gpu_moe_scatter(const float* d_y, const int* d_inv,
  *    expert(x) = down . (silu(gate . x) * (up . x))
  *
  *    A prep launch (unique-expert list, routing weights; with routing, the
- *    router GEMV in workgroups of the same launch), then (a) gate+up+SiLU over every unique expert touched by the M tokens
- *    in one launch, (b) the down projections of all of them in one launch,
- *    whose last workgroup per output row tile adds the per-expert partials
- *    in a fixed order (routing weights are folded in before the down
- *    projection), so repeated calls give identical bits. Weights stream
- *    from the blobs in place; nothing is dequantised to memory. Routing
- *    stays on the device.
+ *    router GEMV in workgroups of the same launch), then (a) gate+up+SiLU
+ *    over every unique expert touched by the M tokens, (b) the down
+ *    projections of all of them, whose last workgroup per output row tile
+ *    adds the partials in a fixed order (routing weights are folded in
+ *    before the down projection), so repeated calls give identical bits.
+ *    (a) and (b) are one launch for one token and hidden <= 4096, two
+ *    otherwise. Weights stream from the blobs in place; nothing is
+ *    dequantised to memory. Routing stays on the device.
  * ======================================================================= */
 
 enum { WISP_DTYPE_F16 = 0, WISP_DTYPE_F32 = 1 };
@@ -233,7 +234,8 @@ hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table,
  * trip: router logits = W x (+ bias), softmax or sigmoid top-k with the
  * rules of wisp_gpu_moe_route, then everything wisp_gpu_moe_decode_int4
  * does. The router GEMV runs in router workgroups of the prep launch
- * (3 launches per layer) when hidden <= 8192 and W and x are 16-byte
+ * (3 launches per layer, 2 for one token with hidden <= 4096, where
+ * gate/up and down share one launch) when hidden <= 8192 and W and x are 16-byte
  * aligned, else in one launch before it. Writes the
  * post-activation scores [n_tokens, n_experts] to d_scores and the
  * selection [n_tokens, top_k] to d_topk_idx / d_topk_w (device), as
@@ -406,9 +408,10 @@ hipError_t wisp_tier_moe_decode_layer(WispExpertTier* t, int layer,
 /* When events != NULL, the fused launchers record events[2*k] before and
  * events[2*k+1] after each kernel of kind k < n_pairs on the launch stream:
  * k = 0 router (wisp_gpu_moe_route, or the router GEMV launch of
- * wisp_gpu_moe_layer_decode_int4), 1 decode prep, 2 decode gate/up,
- * 3 decode down (it also writes the layer output), 4 unused, 5 prefill
- * gate/up, 6 prefill down. Process-wide; for timing runs only; not
+ * wisp_gpu_moe_layer_decode_int4), 1 decode prep, 2 decode gate/up (with
+ * the down projection when both share one launch), 3 decode down (it also
+ * writes the layer output; not recorded when it shares the gate/up
+ * launch), 4 unused, 5 prefill gate/up, 6 prefill down. Process-wide; for timing runs only; not
  * thread-safe. */
 void wisp_amd_set_kernel_events(hipEvent_t* events, int n_pairs);
 

@@ -850,13 +850,14 @@ __device__ __forceinline__ void down_tile(const DecodeParams& P, int q, int rt, 
     if (FUSED)
         hc = __hip_atomic_load(P.hcnt + gu * DEC_HCNT_STRIDE, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
-    u4 xv[M][2];
+    constexpr int XC = NB / 4;   /* 16-byte pieces of the unit's h' per lane and token */
+    u4 xv[M][XC];
     const uint16_t* hsrc = P.hperm + (size_t)u * K + lb0 * 128;
     auto load_h = [&]() {
 #pragma unroll
         for (int v = 0; v < M; v++)
 #pragma unroll
-            for (int c = 0; c < 2; c++) {
+            for (int c = 0; c < XC; c++) {
                 const int i = min(lane + 64 * c, nb * 16 - 1);
                 const uint16_t* src = hsrc + (size_t)v * P.max_u * K + i * 8;
                 if (FUSED) {
@@ -904,7 +905,7 @@ __device__ __forceinline__ void down_tile(const DecodeParams& P, int q, int rt, 
 #pragma unroll
     for (int v = 0; v < M; v++)
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
+        for (int c = 0; c < XC; c++) {
             const int i = lane + 64 * c;
             if (i < nb * 16) *(u4*)(xs + v * L.XR + i * 8) = xv[v][c];
         }
