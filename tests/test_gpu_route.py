@@ -90,7 +90,8 @@ def test_router_vs_oracle(shape, T):
             assert np.allclose(w[t], ow, rtol=1e-4)
 
 
-@pytest.mark.parametrize("T,k,E", [(1, 8, 256), (4, 2, 8), (2048, 8, 256), (37, 6, 1000)])
+@pytest.mark.parametrize("T,k,E", [(1, 8, 256), (4, 2, 8), (2048, 8, 256), (37, 6, 1000),
+                                   (1, 1, 1), (8192, 8, 1024), (3000, 9, 257)])
 def test_expert_offsets_bit_exact(T, k, E):
     print(f"offsets T={T} k={k} E={E}", flush=True)
     rng = np.random.default_rng(T * k)

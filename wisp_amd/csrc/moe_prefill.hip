@@ -98,29 +98,68 @@ __global__ __launch_bounds__(256) void pf_prep_kernel(PfParams P, const void* co
  * 16-token sub-tiles is 2, 4 or 8. */
 __host__ __device__ inline int pf_class(int rows) { return rows <= 32 ? 0 : (rows <= 64 ? 1 : 2); }
 
+#define PF_TILE_THREADS 1024
+#define PF_TILE_EPT (PF_MAX_EXPERTS / PF_TILE_THREADS)   /* experts per thread */
+
 /* One workgroup: tiles of up to PF_BM pairs per expert, experts in order,
- * appended to the list of their class (tiles[c * max_tiles + i]). The
- * counts and offsets are read into LDS by all threads first; one thread
- * then walks them. */
-__global__ __launch_bounds__(256) void pf_tiles_kernel(PfParams P) {
-    __shared__ int s_cnt[PF_MAX_EXPERTS], s_off[PF_MAX_EXPERTS];
+ * appended to the list of their class (tiles[c * max_tiles + i]). An
+ * expert of c pairs gives c / PF_BM full tiles (the last class), then one
+ * tile of the remainder. Thread t takes experts [PF_TILE_EPT t, +PF_TILE_EPT),
+ * counts its tiles per class, and an exclusive scan over the threads per
+ * class gives its first slots, so the lists come out in expert order. */
+__global__ __launch_bounds__(PF_TILE_THREADS) void pf_tiles_kernel(PfParams P) {
+    __shared__ int s_wsum[PF_CLASSES][PF_TILE_THREADS / 64];
     const int E = P.n_experts1;
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        s_cnt[e] = P.counts[e];
-        s_off[e] = P.offsets[e];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    int cnt[PF_TILE_EPT], off[PF_TILE_EPT];
+    int nk[PF_CLASSES] = {0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < PF_TILE_EPT; j++) {
+        const int e = PF_TILE_EPT * tid + j;
+        cnt[j] = e < E ? P.counts[e] : 0;
+        off[j] = e < E ? P.offsets[e] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < PF_TILE_EPT; j++) {
+        nk[PF_CLASSES - 1] += cnt[j] / PF_BM;
+        if (cnt[j] % PF_BM) nk[pf_class(cnt[j] % PF_BM)]++;
+    }
+    int pos[PF_CLASSES], incl[PF_CLASSES];
+#pragma unroll
+    for (int k = 0; k < PF_CLASSES; k++) {
+        int v = nk[k];
+        for (int d = 1; d < 64; d <<= 1) {
+            const int y = __shfl_up(v, d, 64);
+            if (lane >= d) v += y;
+        }
+        incl[k] = v;
+        if (lane == 63) s_wsum[k][wv] = v;
     }
     __syncthreads();
-    if (threadIdx.x != 0) return;
-    int n[PF_CLASSES] = {0, 0, 0};
-    for (int e = 0; e < E; e++) {
-        const int c = s_cnt[e], o = s_off[e];
-        for (int q = 0; q < c; q += PF_BM) {
-            const int rows = min(PF_BM, c - q);
-            const int k = pf_class(rows);
-            if (n[k] < P.max_tiles) P.tiles[k * P.max_tiles + n[k]++] = make_int4(e, o + q, rows, 0);
+#pragma unroll
+    for (int k = 0; k < PF_CLASSES; k++) {
+        for (int w = 0; w < wv; w++) incl[k] += s_wsum[k][w];
+        pos[k] = incl[k] - nk[k];
+    }
+#pragma unroll
+    for (int j = 0; j < PF_TILE_EPT; j++) {
+        const int e = PF_TILE_EPT * tid + j;
+        const int full = cnt[j] / PF_BM, rem = cnt[j] % PF_BM;
+        for (int q = 0; q < full; q++) {
+            const int k = PF_CLASSES - 1;
+            if (pos[k] < P.max_tiles)
+                P.tiles[k * P.max_tiles + pos[k]] = make_int4(e, off[j] + q * PF_BM, PF_BM, 0);
+            pos[k]++;
+        }
+        if (rem) {
+            const int k = pf_class(rem);
+            if (pos[k] < P.max_tiles)
+                P.tiles[k * P.max_tiles + pos[k]] = make_int4(e, off[j] + full * PF_BM, rem, 0);
+            pos[k]++;
         }
     }
-    for (int k = 0; k < PF_CLASSES; k++) P.n_tiles[k] = n[k];
+    if (tid == PF_TILE_THREADS - 1)
+        for (int k = 0; k < PF_CLASSES; k++) P.n_tiles[k] = min(incl[k], P.max_tiles);
 }
 
 /* ======================================================================= */
@@ -502,7 +541,7 @@ extern "C" hipError_t wisp_gpu_moe_prefill_int4(const void* const* d_expert_tabl
     e = wisp_gpu_expert_offsets(P.idx1, n_tokens, P.top_k1, P.n_experts1, P.counts, P.offsets,
                                 P.order, P.inv, s);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(pf_tiles_kernel, dim3(1), dim3(256), 0, s, P);
+    hipLaunchKernelGGL(pf_tiles_kernel, dim3(1), dim3(PF_TILE_THREADS), 0, s, P);
     const bool hz = P.has_zeros != 0;
     /* grid.x per class: an upper bound on its tile count */
     const int np = n_tokens * P.top_k1;

@@ -247,66 +247,104 @@ extern "C" void wisp_gpu_router_topk(const wisp_half* W, const wisp_half* bias, 
 /* expert-offset builder                                                    */
 /* ======================================================================= */
 
-/* One workgroup of T threads; thread t owns the contiguous pair chunk
- * [t*L, (t+1)*L). cnt[t][e] (u16, LDS) counts e in chunk t, then becomes
- * the number of e-pairs in chunks before t. Placement walks each chunk in
- * order, so the result is stable in flat pair order. */
-__global__ void expert_offsets_kernel(const int* __restrict__ topk_idx, int n_pairs,
-                                      int n_experts, int* __restrict__ counts,
-                                      int* __restrict__ offsets, int* __restrict__ order,
-                                      int* __restrict__ inv) {
-    extern __shared__ uint16_t cnt[];            /* [T][n_experts] */
-    __shared__ int s_off[ROUTE_MAX_EXPERTS + 1];
-    const int T = blockDim.x;
-    const int t = threadIdx.x;
-    const int L = (n_pairs + T - 1) / T;
-    const int p0 = min(t * L, n_pairs), p1 = min(p0 + L, n_pairs);
-    for (int i = t; i < T * n_experts; i += T) cnt[i] = 0;
+#define EO_THREADS 1024
+#define EO_WAVES (EO_THREADS / 64)
+#define EO_BATCH 8     /* pairs per lane loaded before any is used */
+
+/* Stable counting sort of the pairs by expert in one workgroup of 16 waves.
+ * Wave w owns the contiguous chunk [w C, w C + C) of pairs, C = ceil(n / 16).
+ * Pass 1 counts each wave's chunk into hist[w][e] (LDS atomics; the order
+ * does not matter for counting). Then thread e turns its column into
+ * running bases, hist[w][e] = number of e-pairs in chunks before w, and the
+ * workgroup scans the totals into offsets. Pass 2: each wave walks its
+ * chunk in order, 64 pairs at a time; lanes holding the same expert find
+ * each other with one ballot per bit of the id, so a pair's position is
+ * offsets[e] + hist[w][e] + the number of such lanes below it, and the
+ * lowest of them advances hist[w][e] by their count (one wave's LDS
+ * operations run in order, so the next group sees it). Flat pair order is
+ * kept within every expert. Loads go out EO_BATCH per lane at a time. */
+__global__ __launch_bounds__(EO_THREADS) void expert_offsets_kernel(
+    const int* __restrict__ topk_idx, int n_pairs, int n_experts, int* __restrict__ counts,
+    int* __restrict__ offsets, int* __restrict__ order, int* __restrict__ inv) {
+    extern __shared__ int eo_lds[];   /* hist [EO_WAVES][E], then off [E] */
+    __shared__ int s_wsum[EO_WAVES];
+    const int E = n_experts;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    int* hist = eo_lds;
+    int* off = eo_lds + EO_WAVES * E;
+    for (int i = tid; i < EO_WAVES * E; i += EO_THREADS) hist[i] = 0;
     __syncthreads();
-    uint16_t* mine = cnt + (size_t)t * n_experts;
-    /* the chunk's ids are loaded 8 at a time: one memory round trip per 8 */
-    for (int p = p0; p < p1; p += 8) {
-        int ev[8];
+    const int C = (n_pairs + EO_WAVES - 1) / EO_WAVES;
+    const int c0 = min(wv * C, n_pairs), c1 = min(c0 + C, n_pairs);
+    for (int base = c0; base < c1; base += 64 * EO_BATCH) {
+        int ev[EO_BATCH];
 #pragma unroll
-        for (int q = 0; q < 8; q++) ev[q] = p + q < p1 ? topk_idx[p + q] : -1;
-#pragma unroll
-        for (int q = 0; q < 8; q++)
-            if (ev[q] >= 0 && ev[q] < n_experts) mine[ev[q]]++;
-    }
-    __syncthreads();
-    /* per-expert exclusive prefix over chunks; totals */
-    for (int e = t; e < n_experts; e += T) {
-        int run = 0;
-        for (int c = 0; c < T; c++) {
-            int v = cnt[(size_t)c * n_experts + e];
-            cnt[(size_t)c * n_experts + e] = (uint16_t)run;
-            run += v;
+        for (int q = 0; q < EO_BATCH; q++) {
+            const int p = base + 64 * q + lane;
+            ev[q] = p < c1 ? topk_idx[p] : -1;
         }
-        counts[e] = run;
-        s_off[e + 1] = run;
+#pragma unroll
+        for (int q = 0; q < EO_BATCH; q++)
+            if (ev[q] >= 0 && ev[q] < E) atomicAdd(&hist[wv * E + ev[q]], 1);
     }
     __syncthreads();
-    if (t == 0) {
-        s_off[0] = 0;
-        for (int e = 0; e < n_experts; e++) s_off[e + 1] += s_off[e];
+    /* column e: running bases over the waves, total in tot */
+    const int e = tid;
+    int tot = 0;
+    if (e < E) {
+        for (int w = 0; w < EO_WAVES; w++) {
+            const int h = hist[w * E + e];
+            hist[w * E + e] = tot;
+            tot += h;
+        }
+    }
+    /* exclusive scan of the totals (E <= EO_THREADS) */
+    int incl = tot;
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += y;
+    }
+    if (lane == 63) s_wsum[wv] = incl;
+    __syncthreads();
+    for (int w = 0; w < wv; w++) incl += s_wsum[w];
+    if (e < E) {
+        off[e] = incl - tot;
+        offsets[e] = incl - tot;
+        counts[e] = tot;
+        if (e == E - 1) offsets[E] = incl;
     }
     __syncthreads();
-    for (int e = t; e <= n_experts; e += T) offsets[e] = s_off[e];
-    for (int p = p0; p < p1; p += 8) {
-        int ev[8];
+    int nbits = 0;
+    while ((1 << nbits) < E) nbits++;
+    const uint64_t lt = (1ull << lane) - 1ull;
+    for (int base = c0; base < c1; base += 64 * EO_BATCH) {
+        int ev[EO_BATCH];
 #pragma unroll
-        for (int q = 0; q < 8; q++) ev[q] = p + q < p1 ? topk_idx[p + q] : -1;
+        for (int q = 0; q < EO_BATCH; q++) {
+            const int p = base + 64 * q + lane;
+            ev[q] = p < c1 ? topk_idx[p] : -1;
+        }
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-            if (p + q >= p1) break;
-            const int e = ev[q];
-            if (e >= 0 && e < n_experts) {
-                const int pos = s_off[e] + mine[e]++;
-                order[pos] = p + q;
-                inv[p + q] = pos;
-            } else {
-                inv[p + q] = -1;
+        for (int q = 0; q < EO_BATCH; q++) {
+            const int p = base + 64 * q + lane;
+            if (base + 64 * q >= c1) break;           /* uniform: past the chunk */
+            const bool valid = p < c1 && ev[q] >= 0 && ev[q] < E;
+            const int ee = valid ? ev[q] : 0;
+            uint64_t peers = __ballot(valid);
+            for (int bit = 0; bit < nbits; bit++) {
+                const bool set = (ee >> bit) & 1;
+                const uint64_t m = __ballot(valid && set);
+                peers &= set ? m : ~m;
             }
+            if (valid) {
+                const int pos = off[ee] + hist[wv * E + ee] + __popcll(peers & lt);
+                order[pos] = p;
+                inv[p] = pos;
+            } else if (p < c1) {
+                inv[p] = -1;
+            }
+            /* the lowest lane of each expert advances the wave's base */
+            if (valid && (peers & lt) == 0) hist[wv * E + ee] += __popcll(peers);
         }
     }
 }
@@ -316,17 +354,14 @@ extern "C" hipError_t wisp_gpu_expert_offsets(const int* d_topk_idx, int n_token
                                               int* d_order, int* d_inv, hipStream_t s) {
     if (n_tokens <= 0 || top_k <= 0 || n_experts <= 0 || n_experts > ROUTE_MAX_EXPERTS)
         return hipErrorInvalidValue;
-    long n_pairs = (long)n_tokens * top_k;
-    /* chunks of at most 65535 pairs per thread (u16 counters) and a count
-     * table of at most 128 KiB of LDS (gfx950 has 160 KiB per workgroup) */
-    int T = 256;
-    while (T > 32 && (size_t)T * n_experts * 2 > 131072) T >>= 1;
-    if ((n_pairs + T - 1) / T > 65535) return hipErrorInvalidValue;
-    size_t lds = (size_t)T * n_experts * sizeof(uint16_t);
+    const long n_pairs = (long)n_tokens * top_k;
+    if (n_pairs > (1L << 30)) return hipErrorInvalidValue;
+    /* hist [16][E] + off [E]: at most 68 KiB of LDS for 1024 experts */
+    const size_t lds = (size_t)(EO_WAVES + 1) * n_experts * sizeof(int);
     if (lds > 65536)
         (void)hipFuncSetAttribute((const void*)expert_offsets_kernel,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL(expert_offsets_kernel, dim3(1), dim3(T), lds, s, d_topk_idx,
+    hipLaunchKernelGGL(expert_offsets_kernel, dim3(1), dim3(EO_THREADS), lds, s, d_topk_idx,
                        (int)n_pairs, n_experts, d_counts, d_offsets, d_order, d_inv);
     return hipGetLastError();
 }
