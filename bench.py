@@ -107,9 +107,10 @@ class Layer:
                                   self.out32.ptr, self.out16.ptr, self.stream.handle)
 
     def fused_experts(self):
-        """True when gate/up and down run in one launch: one token and at
-        most 4 gate/up waves (hidden <= 4096); otherwise two launches."""
-        return self.M == 1 and self.shape.hidden <= 4096
+        """True when gate/up and down run in one launch: one token (any
+        hidden size; above 32 hidden blocks each gate/up row tile's K axis
+        is split over several workgroups); otherwise two launches."""
+        return self.M == 1
 
     def separate_router(self):
         """True when the router GEMV gets its own launch: only for rows longer

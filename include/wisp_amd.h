@@ -198,8 +198,7 @@ hipError_t wisp_gpu_moe_scatter(const float* d_y, const int* d_inv,
  *    projections of all of them, whose last workgroup per output row tile
  *    adds the partials in a fixed order (routing weights are folded in
  *    before the down projection), so repeated calls give identical bits.
- *    (a) and (b) are one launch for one token and hidden <= 4096, two
- *    otherwise. Weights stream from the blobs in place; nothing is
+ *    (a) and (b) are one launch for one token, two otherwise. Weights stream from the blobs in place; nothing is
  *    dequantised to memory. Routing stays on the device.
  * ======================================================================= */
 
@@ -234,8 +233,8 @@ hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table,
  * trip: router logits = W x (+ bias), softmax or sigmoid top-k with the
  * rules of wisp_gpu_moe_route, then everything wisp_gpu_moe_decode_int4
  * does. The router GEMV runs in router workgroups of the prep launch
- * (3 launches per layer, 2 for one token with hidden <= 4096, where
- * gate/up and down share one launch) when hidden <= 8192 and W and x are 16-byte
+ * (3 launches per layer, 2 for one token, where gate/up and down share
+ * one launch) when hidden <= 8192 and W and x are 16-byte
  * aligned, else in one launch before it. Writes the
  * post-activation scores [n_tokens, n_experts] to d_scores and the
  * selection [n_tokens, top_k] to d_topk_idx / d_topk_w (device), as

@@ -103,6 +103,23 @@ def test_dsv3_shape(M):
                idx, w)
 
 
+@pytest.mark.parametrize("hidden,gs,zeros", [(7168, 128, False), (7168, 32, True), (5120, 64, False),
+                                              (4608, 128, True), (12288, 256, False)])
+def test_one_token_split_gate_up(hidden, gs, zeros):
+    """One token with more than 32 hidden blocks: each gate/up row tile's K
+    axis is split over several workgroups (7 blocks per wave at 56 blocks,
+    otherwise 8 with idle waves in the last split); two calls in a row on
+    one workspace give identical results."""
+    print(f"decode split gate/up hidden={hidden} gs={gs} zeros={zeros}", flush=True)
+    rng = np.random.default_rng(hidden + gs)
+    n_exp, k = 16, 4
+    idx = synth.uniform_topk(rng, 1, n_exp, k)
+    w = synth.route_weights(rng, 1, k)
+    a = run_decode(hidden + 3 * gs, 256, hidden, gs, n_exp, k, 1, True, zeros, idx, w)
+    b = run_decode(hidden + 3 * gs, 256, hidden, gs, n_exp, k, 1, True, zeros, idx, w)
+    np.testing.assert_array_equal(a, b)
+
+
 def test_invalid_arguments_are_rejected():
     rng = np.random.default_rng(9)
     blob = synth.make_blob(rng, 256, 512, 128)

@@ -198,7 +198,7 @@ def test_dsv3_layer_m1():
     print("layer dsv3 M=1", flush=True)
     s = synth.DSV3
     run_layer(950, s.inter, s.hidden, s.n_experts, s.top_k, 1, "sigmoid", shared=True,
-              use_bias=False)
+              use_bias=False, repeat=2)
 
 
 def test_nothing_routed_writes_zeros():

@@ -78,6 +78,9 @@ struct DecodeParams {
     float* part;          /* [n_q_max][M][hidden] down partials           */
     int* tile_cnt;        /* [hidden / 16] down workgroups arrived per row tile */
     int* hcnt;            /* [max_u * upe] gate/up workgroups done per wave unit (fused launch) */
+    int gsplit;           /* fused launch: workgroups sharing the K range of one gate/up row tile */
+    int* gcnt;            /* [max_u * inter / 16] split workgroups arrived per gate/up row tile */
+    float* gpart;         /* [max_u * inter / 16][gsplit][2][16] gate/up K-split partials */
     float* out32;         /* [M][hidden] layer output (either may be null) */
     uint16_t* out16;
     int accumulate;
@@ -243,6 +246,8 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     for (int e = threadIdx.x; e < n_experts; e += blockDim.x) s_tab[e] = (const uint8_t*)table[e];
     for (int i = threadIdx.x; i < P.hidden / 16; i += blockDim.x) P.tile_cnt[i] = 0;
     for (int i = threadIdx.x; i < P.max_u * P.upe; i += blockDim.x) P.hcnt[i * DEC_HCNT_STRIDE] = 0;
+    if (P.gsplit > 1)
+        for (int i = threadIdx.x; i < P.max_u * (P.inter / 16); i += blockDim.x) P.gcnt[i] = 0;
     /* x -> fp16 copy when the gate/up kernel cannot read the caller's x */
     if (P.xconv) {
         for (int i = threadIdx.x; i < M * P.hidden; i += blockDim.x)
@@ -609,14 +614,15 @@ __device__ __forceinline__ void compute_blocks(const u4 (&w)[NB][NT], const uint
     }
 }
 
-/* Copies M activation rows [M][K] (fp16) into the LDS x image, permuting
- * each 8-element block into unpack8_magic slot order with odd elements
- * divided by 16 (exact: a power-of-two scale). 16-byte accesses. */
+/* Copies the first `len` elements of M activation rows (fp16, row stride
+ * K) into the LDS x image, permuting each 8-element block into
+ * unpack8_magic slot order with odd elements divided by 16 (exact: a
+ * power-of-two scale). 16-byte accesses. */
 template <int M>
 __device__ __forceinline__ void stage_x_perm(uint8_t* smem, const LdsMap& L,
-                                             const uint16_t* __restrict__ src, int K) {
+                                             const uint16_t* __restrict__ src, int K, int len) {
     uint16_t* xs = (uint16_t*)(smem + L.x_off);
-    const int per_row = K / 8;
+    const int per_row = len / 8;
     const f16 sixteenth = (f16)0.0625f;
     for (int i = threadIdx.x; i < M * per_row; i += blockDim.x) {
         const int v = i / per_row, c = i - v * per_row;
@@ -633,12 +639,18 @@ __device__ __forceinline__ void stage_x_perm(uint8_t* smem, const LdsMap& L,
 /* ======================================================================= */
 
 /* One gate/up workgroup: TILES gate + TILES up row tiles starting at row
- * 16 TILES rt of unique expert u over the full hidden K, waves split K. In
- * the fused launch (FUSED) h' is written with device-coherent stores and,
- * once they are acknowledged, the workgroup counts itself on its wave
- * unit's counter (the down waves of the same launch poll it). */
+ * 16 TILES rt of unique expert u, over K blocks [nw NB split, nw NB (split
+ * + 1)) of the hidden axis (split 0 of 1: the full K), waves split that
+ * range. In the fused launch (FUSED) h' is written with device-coherent
+ * stores and, once they are acknowledged, the workgroup counts itself on
+ * its wave unit's counter (the down waves of the same launch poll it).
+ * With P.gsplit > 1 workgroups sharing a row tile (fused launch, TILES = 1,
+ * one token), each stores its gate and up partial sums with
+ * device-coherent stores and counts itself on the tile's counter; the last
+ * to arrive adds the partials in split order and finishes the tile. */
 template <int M, int NG, int TILES, int NB, bool HZ, bool FUSED>
-__device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt, uint8_t* smem) {
+__device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt, int split,
+                                            uint8_t* smem) {
     constexpr int NT = 2 * TILES;
     /* both loads in one round trip (slot u < max_u always exists) */
     const int n_u = *P.n_unique;
@@ -650,8 +662,11 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
     const int r0 = rt * 16 * TILES;
     const int nblk = K >> 7;
     const int G = K / P.gs;
-    /* wave w owns blocks [NB w, NB w + NB); the host launches ceil(nblk/NB) waves */
-    const int b0 = wave * NB, b1 = min(b0 + NB, nblk);
+    /* wave w owns blocks [xb0 + NB w, xb0 + NB w + NB); the host launches
+     * min(4, ceil(nblk / NB)) waves and gsplit = ceil(nblk / (waves NB)) */
+    const int xb0 = split * nw * NB;
+    const int xlen = min(nw * NB, nblk - xb0);      /* blocks of this split */
+    const int b0 = xb0 + wave * NB, b1 = min(b0 + NB, nblk);
     const LdsMap L = lds_map(M, NT, K, G, HZ, nw);
 
     const uint8_t* wp[NT];
@@ -664,13 +679,13 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
      * the whole workgroup), then all of this wave's weights; the LDS writes
      * then wait only for the former. The scales (and zeros) of 16
      * consecutive rows are one contiguous run of 32 G bytes. */
-    constexpr int XCNT = M * NB / 4 > 0 ? M * NB / 4 : 1;
+    constexpr int XCNT = (M * NB + 3) / 4;
     constexpr int SCNT = NB * NG / 16 > 0 ? NB * NG / 16 : 1;
     Stage16<XCNT> sx;
     Stage16<SCNT> ssc[NT], szc[NT];
-    const bool fast = Stage16<XCNT>::ok(M, K / 8) && Stage16<SCNT>::ok(1, 2 * G);
+    const bool fast = Stage16<XCNT>::ok(M, xlen * 16) && Stage16<SCNT>::ok(1, 2 * G);
     if (fast) {
-        sx.issue((const uint8_t*)P.xh, (size_t)K * 2, M, K / 8);
+        sx.issue((const uint8_t*)(P.xh + xb0 * 128), (size_t)K * 2, M, xlen * 16);
 #pragma unroll
         for (int s = 0; s < NT; s++) {
             const int mat = s < TILES ? 0 : 1;
@@ -689,7 +704,7 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
             if (HZ) szc[s].template commit<false>(smem + L.zc_off + s * 32 * G, 0);
         }
     } else {
-        stage_x_perm<M>(smem, L, P.xh, K);
+        stage_x_perm<M>(smem, L, P.xh + xb0 * 128, K, xlen * 128);
 #pragma unroll
         for (int s = 0; s < NT; s++) {
             const int mat = s < TILES ? 0 : 1;
@@ -708,8 +723,8 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
     for (int s = 0; s < NT; s++)
 #pragma unroll
         for (int v = 0; v < M; v++) tot[s][v] = 0.0f;
-    compute_blocks<M, NG, NT, NB, HZ>(w, smem, L, b0, b1, 0, 0, P.gshift, col, j, P.m_lo, P.m_hi,
-                                      P.one024, tot);
+    compute_blocks<M, NG, NT, NB, HZ>(w, smem, L, b0, b1, xb0, 0, P.gshift, col, j, P.m_lo,
+                                      P.m_hi, P.one024, tot);
 
     float* red = (float*)(smem + L.red_off);
     if (lane < 16) {
@@ -719,12 +734,44 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
             for (int v = 0; v < M; v++) red[((wave * NT + s) * 16 + col) * M + v] = tot[s][v];
     }
     __syncthreads();
+    const int n_split = (FUSED && M == 1 && TILES == 1) ? P.gsplit : 1;
+    const int tile_id = u * (P.inter / (16 * TILES)) + rt;
+    if (n_split > 1) {
+        /* K-split: publish this split's sums; the last arrival finishes */
+        __shared__ int s_glast;
+        for (int o = threadIdx.x; o < 16; o += blockDim.x) {
+            float g = 0.0f, up = 0.0f;
+            for (int ww = 0; ww < nw; ww++) {
+                g += red[(ww * NT) * 16 + o];
+                up += red[(ww * NT + 1) * 16 + o];
+            }
+            float* dst = P.gpart + ((size_t)tile_id * n_split + split) * 32;
+            __hip_atomic_store(dst + o, g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(dst + 16 + o, up, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_s_waitcnt(0);   /* this thread's partial stores are acknowledged */
+        __syncthreads();
+        if (threadIdx.x == 0)
+            s_glast = __hip_atomic_fetch_add(P.gcnt + tile_id, 1, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT) == n_split - 1;
+        __syncthreads();
+        if (!s_glast) return;
+    }
     for (int o = threadIdx.x; o < TILES * 16 * M; o += blockDim.x) {
         const int v = o % M, rc = o / M, q = rc / 16, c = rc % 16;
         float g = 0.0f, up = 0.0f;
-        for (int ww = 0; ww < nw; ww++) {
-            g += red[((ww * NT + q) * 16 + c) * M + v];
-            up += red[((ww * NT + TILES + q) * 16 + c) * M + v];
+        if (n_split > 1) {
+            const float* src = P.gpart + (size_t)tile_id * n_split * 32;
+            for (int sp = 0; sp < n_split; sp++) {
+                g += __hip_atomic_load(src + sp * 32 + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                up += __hip_atomic_load(src + sp * 32 + 16 + c, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+            }
+        } else {
+            for (int ww = 0; ww < nw; ww++) {
+                g += red[((ww * NT + q) * 16 + c) * M + v];
+                up += red[((ww * NT + TILES + q) * 16 + c) * M + v];
+            }
         }
         const float h = silu_f(g) * up * P.uw[u * 4 + v];
         const int r = r0 + 16 * q + c;
@@ -750,7 +797,7 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
 template <int M, int NG, int TILES, int NB, bool HZ>
 __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void gateup_kernel(const DecodeParams P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    gateup_tile<M, NG, TILES, NB, HZ, false>(P, blockIdx.y, blockIdx.x, smem);
+    gateup_tile<M, NG, TILES, NB, HZ, false>(P, blockIdx.y, blockIdx.x, 0, smem);
 }
 
 /* ======================================================================= */
@@ -974,8 +1021,10 @@ __global__ __launch_bounds__(64 * DN_WAVES) void down_kernel(const DecodeParams 
     down_tile<M, NG, HZ, false>(P, blockIdx.y, blockIdx.x, smem);
 }
 
-/* One launch for gate/up and down: the first max_u * inter / 16 workgroups
- * are gate/up workgroups (expert-major, so an expert's h' completes early),
+/* One launch for gate/up and down: the first max_u * inter / 16 * gsplit
+ * workgroups are gate/up workgroups (expert-major, then row tile, then K
+ * split, so an expert's h' completes early and the splits of a row tile
+ * arrive together),
  * the rest down workgroups (chunk-major); a workgroup has as many waves as
  * gate/up needs, which is also the down chunk's unit count. Down waves wait
  * only on workgroups earlier in the grid, which wait on nothing, so every
@@ -984,10 +1033,12 @@ template <int M, int NG, int NB, bool HZ>
 __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void expert_kernel(const DecodeParams P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int n_rt = P.inter / 16;
-    const int n_gu = P.max_u * n_rt;
+    const int per_u = n_rt * P.gsplit;
+    const int n_gu = P.max_u * per_u;
     const int b = blockIdx.x;
     if (b < n_gu) {
-        gateup_tile<M, NG, 1, NB, HZ, true>(P, b / n_rt, b % n_rt, smem);
+        const int u = b / per_u, r = b - u * per_u;
+        gateup_tile<M, NG, 1, NB, HZ, true>(P, u, r / P.gsplit, r % P.gsplit, smem);
     } else {
         const int d = b - n_gu, n_ro = P.hidden / 16;
         down_tile<M, NG, HZ, true>(P, d / n_ro, d % n_ro, smem);
@@ -1024,9 +1075,32 @@ extern "C" hipError_t wisp_expert_layout_check(const WispExpertLayout* L) {
 }
 
 struct WsLayout {
-    size_t nu, epoch, tile_cnt, hcnt, ublob, uw, xconv, hperm, part, rwords, total;
+    size_t nu, epoch, tile_cnt, hcnt, ublob, uw, xconv, hperm, part, rwords, gcnt, gpart, total;
     int max_u, n_q_max;
 };
+
+/* Shape of the one-launch gate/up + down for one token: 4-wave workgroups
+ * (fewer when the hidden axis has fewer than 32 blocks); a gate/up row tile
+ * whose K axis needs more than 4 waves of 8 blocks is split over gsplit
+ * workgroups of 4 waves x nb blocks (DeepSeek-V3, 56 blocks: 2 x 4 x 7). */
+struct FusedShape {
+    int waves, nb, gsplit;
+};
+static FusedShape fused_shape(int nblk) {
+    FusedShape f;
+    if (nblk <= 32) {
+        f.nb = 8;
+        f.waves = (nblk + 7) / 8;
+        f.gsplit = 1;
+        return f;
+    }
+    f.waves = 4;
+    f.gsplit = (nblk + 31) / 32;
+    f.nb = (nblk + 4 * f.gsplit - 1) / (4 * f.gsplit);
+    if (f.nb != 7) f.nb = 8;   /* compiled: 7 or 8 blocks per wave */
+    f.gsplit = (nblk + 4 * f.nb - 1) / (4 * f.nb);
+    return f;
+}
 
 static WsLayout ws_layout(const WispExpertLayout* L, int M, int top_k, int has_shared) {
     WsLayout w;
@@ -1045,6 +1119,10 @@ static WsLayout ws_layout(const WispExpertLayout* L, int M, int top_k, int has_s
     w.part = off; off = align_up(off + (size_t)w.n_q_max * M * L->cols[0] * 4, 256);
     w.hcnt = off; off = align_up(off + (size_t)w.max_u * upe * DEC_HCNT_STRIDE * sizeof(int), 256);
     w.rwords = off; off = align_up(off + (size_t)M * DEC_ROUTE_MAX_EXPERTS * 8, 256);
+    const size_t gtiles = (size_t)w.max_u * (L->rows[0] / 16);
+    const int gsplit = M == 1 ? fused_shape((int)(L->cols[0] / 128)).gsplit : 1;
+    w.gcnt = off; off = align_up(off + (gsplit > 1 ? gtiles * sizeof(int) : 0), 256);
+    w.gpart = off; off = align_up(off + (gsplit > 1 ? gtiles * gsplit * 32 * sizeof(float) : 0), 256);
     w.total = off;
     return w;
 }
@@ -1056,8 +1134,8 @@ extern "C" size_t wisp_moe_decode_workspace_bytes(const WispExpertLayout* L, int
     return ws_layout(L, n_tokens, top_k, has_shared).total;
 }
 
-/* Blocks of 128 weights per wave: each wave issues all its weight loads at
- * once (NB x 16 B per row tile and lane). */
+/* Blocks of 128 weights per wave of the separate gate/up launch: each wave
+ * issues all its weight loads at once (NB x 16 B per row tile and lane). */
 static int blocks_per_wave(int nblk) { return nblk > 8 * DEC_MAX_WAVES ? 16 : 8; }
 
 template <int M, int NG, int TILES, int NB, bool HZ>
@@ -1080,8 +1158,7 @@ static void launch_down(DecodeParams P, hipStream_t s) {
 
 /* gate/up and down in one launch (expert_kernel) */
 template <int M, int NG, int NB, bool HZ>
-static void launch_fused(DecodeParams P, hipStream_t s) {
-    const int waves = (P.hidden / 128 + NB - 1) / NB;
+static void launch_fused(DecodeParams P, int waves, hipStream_t s) {
     P.n_q_max = (P.max_u * P.upe + waves - 1) / waves;
     const LdsMap Lg = lds_map(M, 2, P.hidden, P.hidden / P.gs, HZ, waves);
     const LdsMap Ld = down_wave_map(M, DEC_UNIT_BLOCKS * NG, HZ, 0, waves);
@@ -1089,27 +1166,26 @@ static void launch_fused(DecodeParams P, hipStream_t s) {
     auto k = expert_kernel<M, NG, NB, HZ>;
     if (lds > 65536)
         (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    const int grid = P.max_u * (P.inter / 16) + P.n_q_max * (P.hidden / 16);
+    const int grid = P.max_u * (P.inter / 16) * P.gsplit + P.n_q_max * (P.hidden / 16);
     hipLaunchKernelGGL(k, dim3(grid), dim3(64 * waves), lds, s, P);
 }
 
-/* One launch for gate/up and down when the gate/up workgroup leaves the
- * down role its occupancy: one token and at most 4 waves (hidden <= 4096).
- * The fused kernel takes the larger register budget and wave count of the
- * two roles; with more tokens (more registers) or more waves (DeepSeek-V3's
- * 7) its down waves ran at half the occupancy of the down kernel alone and
- * the layer got slower (DeepSeek-V3 M=4: 281.6 against 224.7 us). */
+/* One launch for gate/up and down for one token, in 4-wave workgroups
+ * (fused_shape; P.gsplit was set from it). The fused kernel takes the
+ * larger register budget of the two roles; with more tokens (more
+ * registers) its down waves ran at half the occupancy of the down kernel
+ * alone and the layer got slower (DeepSeek-V3 M=4: 281.6 against
+ * 224.7 us), so M > 1 keeps two launches. */
 template <int M, int NG, bool HZ>
 static void launch_compute(const DecodeParams& P, hipStream_t s) {
     const int nbw = blocks_per_wave(P.hidden / 128);
-    const int waves = (P.hidden / 128 + nbw - 1) / nbw;
     if constexpr (M == 1) {
-        if (waves <= 4) {
-            ev_before(EV_GATEUP, s);
-            launch_fused<M, NG, 8, HZ>(P, s);
-            ev_after(EV_GATEUP, s);
-            return;
-        }
+        const FusedShape f = fused_shape(P.hidden / 128);
+        ev_before(EV_GATEUP, s);
+        if (f.nb == 7) launch_fused<M, NG, 7, HZ>(P, f.waves, s);
+        else launch_fused<M, NG, 8, HZ>(P, f.waves, s);
+        ev_after(EV_GATEUP, s);
+        return;
     }
     ev_before(EV_GATEUP, s);
     if (nbw == 16) launch_gateup<M, NG, 1, 16, HZ>(P, s);
@@ -1179,6 +1255,9 @@ static hipError_t decode_run(const void* const* d_expert_table, const void* d_sh
     P.xh = x_direct ? (const uint16_t*)d_x : P.xconv;
     P.hperm = (uint16_t*)(ws + w.hperm);
     P.part = (float*)(ws + w.part);
+    P.gsplit = M == 1 ? fused_shape(P.hidden / 128).gsplit : 1;
+    P.gcnt = (int*)(ws + w.gcnt);
+    P.gpart = (float*)(ws + w.gpart);
     P.out32 = d_out_f32;
     P.out16 = (uint16_t*)d_out_f16;
     P.accumulate = accumulate ? 1 : 0;
