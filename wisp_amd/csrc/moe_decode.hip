@@ -734,12 +734,17 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
             for (int v = 0; v < M; v++) red[((wave * NT + s) * 16 + col) * M + v] = tot[s][v];
     }
     __syncthreads();
+    /* Wave 0 finishes the tile (at most 64 outputs, one per lane); the
+     * other waves end here, so their registers take new workgroups while
+     * wave 0's hand-off round trips run. No barrier follows. */
+    static_assert(TILES * 16 * M <= 64, "one wave finishes the tile");
+    if (wave != 0) return;
     const int n_split = (FUSED && M == 1 && TILES == 1) ? P.gsplit : 1;
     const int tile_id = u * (P.inter / (16 * TILES)) + rt;
     if (n_split > 1) {
         /* K-split: publish this split's sums; the last arrival finishes */
-        __shared__ int s_glast;
-        for (int o = threadIdx.x; o < 16; o += blockDim.x) {
+        if (lane < 16) {
+            const int o = lane;
             float g = 0.0f, up = 0.0f;
             for (int ww = 0; ww < nw; ww++) {
                 g += red[(ww * NT) * 16 + o];
@@ -749,15 +754,15 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
             __hip_atomic_store(dst + o, g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(dst + 16 + o, up, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        __builtin_amdgcn_s_waitcnt(0);   /* this thread's partial stores are acknowledged */
-        __syncthreads();
-        if (threadIdx.x == 0)
-            s_glast = __hip_atomic_fetch_add(P.gcnt + tile_id, 1, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT) == n_split - 1;
-        __syncthreads();
-        if (!s_glast) return;
+        __builtin_amdgcn_s_waitcnt(0);   /* the wave's partial stores are acknowledged */
+        int last = 0;
+        if (lane == 0)
+            last = __hip_atomic_fetch_add(P.gcnt + tile_id, 1, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT) == n_split - 1;
+        if (!__builtin_amdgcn_readfirstlane(last)) return;
     }
-    for (int o = threadIdx.x; o < TILES * 16 * M; o += blockDim.x) {
+    if (lane < TILES * 16 * M) {
+        const int o = lane;
         const int v = o % M, rc = o / M, q = rc / 16, c = rc % 16;
         float g = 0.0f, up = 0.0f;
         if (n_split > 1) {
@@ -785,9 +790,8 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
             *dst = __builtin_bit_cast(uint16_t, hv);
     }
     if (FUSED) {
-        __builtin_amdgcn_s_waitcnt(0);   /* this thread's h' stores are acknowledged */
-        __syncthreads();
-        if (threadIdx.x == 0)
+        __builtin_amdgcn_s_waitcnt(0);   /* the wave's h' stores are acknowledged */
+        if (lane == 0)
             __hip_atomic_fetch_add(P.hcnt + (u * P.upe + r0 / (DEC_UNIT_BLOCKS * 128)) * DEC_HCNT_STRIDE, 1,
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -853,7 +857,6 @@ template <int M, int NG, bool HZ, bool FUSED>
 __device__ __forceinline__ void down_tile(const DecodeParams& P, int q, int rt, uint8_t* smem) {
     constexpr int NB = DEC_UNIT_BLOCKS;
     constexpr int GMAX = NB * NG;
-    __shared__ int s_last;
     const int r0 = rt * 16;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int col = lane & 15, j = lane >> 4;
@@ -980,22 +983,26 @@ __device__ __forceinline__ void down_tile(const DecodeParams& P, int q, int rt, 
         for (int v = 0; v < M; v++) red[(wave * 16 + col) * M + v] = tot[0][v];
     }
     __syncthreads();
-    for (int o = threadIdx.x; o < 16 * M; o += blockDim.x) {
+    /* Wave 0 finishes (16 M <= 64 outputs); the other waves end here and
+     * free their registers for new workgroups. No barrier follows. */
+    if (wave != 0) return;
+    if (lane < 16 * M) {
+        const int o = lane;
         const int v = o % M, cc = o / M;
         float y = 0.0f;
         for (int ww = 0; ww < nw; ww++) y += red[(ww * 16 + cc) * M + v];
         __hip_atomic_store(P.part + ((size_t)q * M + v) * H + r0 + cc, y, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     }
-    __builtin_amdgcn_s_waitcnt(0);   /* this thread's partial stores are acknowledged */
-    __syncthreads();
-    if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(P.tile_cnt + rt, 1, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT) == n_q - 1;
-    __syncthreads();
-    if (!s_last) return;
+    __builtin_amdgcn_s_waitcnt(0);   /* the wave's partial stores are acknowledged */
+    int last = 0;
+    if (lane == 0)
+        last = __hip_atomic_fetch_add(P.tile_cnt + rt, 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == n_q - 1;
+    if (!__builtin_amdgcn_readfirstlane(last)) return;
     constexpr int MAXQ = 16;
-    for (int o = threadIdx.x; o < 16 * M; o += blockDim.x) {
+    if (lane < 16 * M) {
+        const int o = lane;
         const int v = o / 16, r = r0 + o % 16;
         const float* src = P.part + (size_t)v * H + r;
         const size_t stride = (size_t)M * H;
