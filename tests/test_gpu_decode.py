@@ -103,20 +103,24 @@ def test_dsv3_shape(M):
                idx, w)
 
 
-@pytest.mark.parametrize("hidden,gs,zeros", [(7168, 128, False), (7168, 32, True), (5120, 64, False),
-                                              (4608, 128, True), (12288, 256, False)])
-def test_one_token_split_gate_up(hidden, gs, zeros):
-    """One token with more than 32 hidden blocks: each gate/up row tile's K
-    axis is split over several workgroups (7 blocks per wave at 56 blocks,
-    otherwise 8 with idle waves in the last split); two calls in a row on
-    one workspace give identical results."""
-    print(f"decode split gate/up hidden={hidden} gs={gs} zeros={zeros}", flush=True)
-    rng = np.random.default_rng(hidden + gs)
+@pytest.mark.parametrize("hidden,gs,zeros,M", [(7168, 128, False, 1), (7168, 32, True, 1),
+                                                (5120, 64, False, 1), (4608, 128, True, 1),
+                                                (12288, 256, False, 1), (7168, 128, True, 2),
+                                                (7168, 64, False, 3), (7168, 128, False, 4),
+                                                (12288, 128, True, 4), (5120, 128, False, 2)])
+def test_split_gate_up(hidden, gs, zeros, M):
+    """More than 32 hidden blocks: each gate/up row tile's K axis is split
+    over several workgroups (7 blocks per wave at 56 blocks, otherwise 8 with
+    idle waves in the last split), for one token in the one-launch kernel and
+    for 2-4 tokens in the separate gate/up launch; two calls in a row on one
+    workspace give identical results."""
+    print(f"decode split gate/up hidden={hidden} gs={gs} zeros={zeros} M={M}", flush=True)
+    rng = np.random.default_rng(hidden + gs + M)
     n_exp, k = 16, 4
-    idx = synth.uniform_topk(rng, 1, n_exp, k)
-    w = synth.route_weights(rng, 1, k)
-    a = run_decode(hidden + 3 * gs, 256, hidden, gs, n_exp, k, 1, True, zeros, idx, w)
-    b = run_decode(hidden + 3 * gs, 256, hidden, gs, n_exp, k, 1, True, zeros, idx, w)
+    idx = synth.uniform_topk(rng, M, n_exp, k)
+    w = synth.route_weights(rng, M, k)
+    a = run_decode(hidden + 3 * gs + M, 256, hidden, gs, n_exp, k, M, True, zeros, idx, w)
+    b = run_decode(hidden + 3 * gs + M, 256, hidden, gs, n_exp, k, M, True, zeros, idx, w)
     np.testing.assert_array_equal(a, b)
 
 

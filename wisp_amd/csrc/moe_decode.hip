@@ -78,9 +78,9 @@ struct DecodeParams {
     float* part;          /* [n_q_max][M][hidden] down partials           */
     int* tile_cnt;        /* [hidden / 16] down workgroups arrived per row tile */
     int* hcnt;            /* [max_u * upe] gate/up workgroups done per wave unit (fused launch) */
-    int gsplit;           /* fused launch: workgroups sharing the K range of one gate/up row tile */
+    int gsplit;           /* workgroups sharing the K range of one gate/up row tile */
     int* gcnt;            /* [max_u * inter / 16] split workgroups arrived per gate/up row tile */
-    float* gpart;         /* [max_u * inter / 16][gsplit][2][16] gate/up K-split partials */
+    float* gpart;         /* [max_u * inter / 16][gsplit][2][16][M] gate/up K-split partials */
     float* out32;         /* [M][hidden] layer output (either may be null) */
     uint16_t* out16;
     int accumulate;
@@ -644,10 +644,10 @@ __device__ __forceinline__ void stage_x_perm(uint8_t* smem, const LdsMap& L,
  * range. In the fused launch (FUSED) h' is written with device-coherent
  * stores and, once they are acknowledged, the workgroup counts itself on
  * its wave unit's counter (the down waves of the same launch poll it).
- * With P.gsplit > 1 workgroups sharing a row tile (fused launch, TILES = 1,
- * one token), each stores its gate and up partial sums with
- * device-coherent stores and counts itself on the tile's counter; the last
- * to arrive adds the partials in split order and finishes the tile. */
+ * With P.gsplit > 1 workgroups sharing a row tile (TILES = 1), each stores
+ * its gate and up partial sums with device-coherent stores and counts
+ * itself on the tile's counter; the last to arrive adds the partials in
+ * split order and finishes the tile. */
 template <int M, int NG, int TILES, int NB, bool HZ, bool FUSED>
 __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt, int split,
                                             uint8_t* smem) {
@@ -667,7 +667,7 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
     const int xb0 = split * nw * NB;
     const int xlen = min(nw * NB, nblk - xb0);      /* blocks of this split */
     const int b0 = xb0 + wave * NB, b1 = min(b0 + NB, nblk);
-    const LdsMap L = lds_map(M, NT, K, G, HZ, nw);
+    const LdsMap L = lds_map(M, NT, min(K, nw * NB * 128), G, HZ, nw);
 
     const uint8_t* wp[NT];
 #pragma unroll
@@ -739,20 +739,21 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
      * wave 0's hand-off round trips run. No barrier follows. */
     static_assert(TILES * 16 * M <= 64, "one wave finishes the tile");
     if (wave != 0) return;
-    const int n_split = (FUSED && M == 1 && TILES == 1) ? P.gsplit : 1;
+    const int n_split = TILES == 1 ? P.gsplit : 1;
     const int tile_id = u * (P.inter / (16 * TILES)) + rt;
     if (n_split > 1) {
-        /* K-split: publish this split's sums; the last arrival finishes */
-        if (lane < 16) {
-            const int o = lane;
+        /* K-split: publish this split's sums (lane = 16-row index * M +
+         * token); the last arrival finishes */
+        if (lane < 16 * M) {
+            const int o = lane, v = o % M, c = o / M;
             float g = 0.0f, up = 0.0f;
             for (int ww = 0; ww < nw; ww++) {
-                g += red[(ww * NT) * 16 + o];
-                up += red[(ww * NT + 1) * 16 + o];
+                g += red[((ww * NT) * 16 + c) * M + v];
+                up += red[((ww * NT + 1) * 16 + c) * M + v];
             }
-            float* dst = P.gpart + ((size_t)tile_id * n_split + split) * 32;
+            float* dst = P.gpart + ((size_t)tile_id * n_split + split) * 32 * M;
             __hip_atomic_store(dst + o, g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(dst + 16 + o, up, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(dst + 16 * M + o, up, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         __builtin_amdgcn_s_waitcnt(0);   /* the wave's partial stores are acknowledged */
         int last = 0;
@@ -766,10 +767,11 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
         const int v = o % M, rc = o / M, q = rc / 16, c = rc % 16;
         float g = 0.0f, up = 0.0f;
         if (n_split > 1) {
-            const float* src = P.gpart + (size_t)tile_id * n_split * 32;
+            const float* src = P.gpart + (size_t)tile_id * n_split * 32 * M;
             for (int sp = 0; sp < n_split; sp++) {
-                g += __hip_atomic_load(src + sp * 32 + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                up += __hip_atomic_load(src + sp * 32 + 16 + c, __ATOMIC_RELAXED,
+                g += __hip_atomic_load(src + sp * 32 * M + o, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                up += __hip_atomic_load(src + sp * 32 * M + 16 * M + o, __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_AGENT);
             }
         } else {
@@ -797,11 +799,13 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
     }
 }
 
-/* grid (inter / (16 TILES), max_u): gate/up of unique expert blockIdx.y. */
+/* grid (inter / (16 TILES) * gsplit, max_u): gate/up of unique expert
+ * blockIdx.y, row tile blockIdx.x / gsplit, K split blockIdx.x % gsplit. */
 template <int M, int NG, int TILES, int NB, bool HZ>
 __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void gateup_kernel(const DecodeParams P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    gateup_tile<M, NG, TILES, NB, HZ, false>(P, blockIdx.y, blockIdx.x, 0, smem);
+    gateup_tile<M, NG, TILES, NB, HZ, false>(P, blockIdx.y, blockIdx.x / P.gsplit,
+                                             blockIdx.x % P.gsplit, smem);
 }
 
 /* ======================================================================= */
@@ -1086,10 +1090,11 @@ struct WsLayout {
     int max_u, n_q_max;
 };
 
-/* Shape of the one-launch gate/up + down for one token: 4-wave workgroups
- * (fewer when the hidden axis has fewer than 32 blocks); a gate/up row tile
- * whose K axis needs more than 4 waves of 8 blocks is split over gsplit
- * workgroups of 4 waves x nb blocks (DeepSeek-V3, 56 blocks: 2 x 4 x 7). */
+/* Shape of the gate/up workgroups: 4 waves (fewer when the hidden axis has
+ * fewer than 32 blocks); a row tile whose K axis needs more than 4 waves of
+ * 8 blocks is split over gsplit workgroups of 4 waves x nb blocks
+ * (DeepSeek-V3, 56 blocks: 2 x 4 x 7). Measured against one workgroup of 7
+ * waves per row tile: DeepSeek-V3 one token 55.2 -> 51.5 us per layer. */
 struct FusedShape {
     int waves, nb, gsplit;
 };
@@ -1127,9 +1132,10 @@ static WsLayout ws_layout(const WispExpertLayout* L, int M, int top_k, int has_s
     w.hcnt = off; off = align_up(off + (size_t)w.max_u * upe * DEC_HCNT_STRIDE * sizeof(int), 256);
     w.rwords = off; off = align_up(off + (size_t)M * DEC_ROUTE_MAX_EXPERTS * 8, 256);
     const size_t gtiles = (size_t)w.max_u * (L->rows[0] / 16);
-    const int gsplit = M == 1 ? fused_shape((int)(L->cols[0] / 128)).gsplit : 1;
+    const int gsplit = fused_shape((int)(L->cols[0] / 128)).gsplit;
     w.gcnt = off; off = align_up(off + (gsplit > 1 ? gtiles * sizeof(int) : 0), 256);
-    w.gpart = off; off = align_up(off + (gsplit > 1 ? gtiles * gsplit * 32 * sizeof(float) : 0), 256);
+    w.gpart = off;
+    off = align_up(off + (gsplit > 1 ? gtiles * gsplit * 32 * M * sizeof(float) : 0), 256);
     w.total = off;
     return w;
 }
@@ -1141,18 +1147,15 @@ extern "C" size_t wisp_moe_decode_workspace_bytes(const WispExpertLayout* L, int
     return ws_layout(L, n_tokens, top_k, has_shared).total;
 }
 
-/* Blocks of 128 weights per wave of the separate gate/up launch: each wave
- * issues all its weight loads at once (NB x 16 B per row tile and lane). */
-static int blocks_per_wave(int nblk) { return nblk > 8 * DEC_MAX_WAVES ? 16 : 8; }
-
 template <int M, int NG, int TILES, int NB, bool HZ>
-static void launch_gateup(const DecodeParams& P, hipStream_t s) {
-    const int waves = (P.hidden / 128 + NB - 1) / NB;
-    const LdsMap L = lds_map(M, 2 * TILES, P.hidden, P.hidden / P.gs, HZ, waves);
+static void launch_gateup(const DecodeParams& P, int waves, hipStream_t s) {
+    const int xk = P.hidden < waves * NB * 128 ? P.hidden : waves * NB * 128;
+    const LdsMap L = lds_map(M, 2 * TILES, xk, P.hidden / P.gs, HZ, waves);
     auto k = gateup_kernel<M, NG, TILES, NB, HZ>;
     if (L.bytes > 65536)
         (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, L.bytes);
-    hipLaunchKernelGGL(k, dim3(P.inter / (16 * TILES), P.max_u), dim3(64 * waves), L.bytes, s, P);
+    hipLaunchKernelGGL(k, dim3(P.inter / (16 * TILES) * P.gsplit, P.max_u), dim3(64 * waves),
+                       L.bytes, s, P);
 }
 
 template <int M, int NG, bool HZ>
@@ -1167,7 +1170,8 @@ static void launch_down(DecodeParams P, hipStream_t s) {
 template <int M, int NG, int NB, bool HZ>
 static void launch_fused(DecodeParams P, int waves, hipStream_t s) {
     P.n_q_max = (P.max_u * P.upe + waves - 1) / waves;
-    const LdsMap Lg = lds_map(M, 2, P.hidden, P.hidden / P.gs, HZ, waves);
+    const int xk = P.hidden < waves * NB * 128 ? P.hidden : waves * NB * 128;
+    const LdsMap Lg = lds_map(M, 2, xk, P.hidden / P.gs, HZ, waves);
     const LdsMap Ld = down_wave_map(M, DEC_UNIT_BLOCKS * NG, HZ, 0, waves);
     const int lds = Lg.bytes > Ld.bytes ? Lg.bytes : Ld.bytes;
     auto k = expert_kernel<M, NG, NB, HZ>;
@@ -1185,9 +1189,8 @@ static void launch_fused(DecodeParams P, int waves, hipStream_t s) {
  * 224.7 us), so M > 1 keeps two launches. */
 template <int M, int NG, bool HZ>
 static void launch_compute(const DecodeParams& P, hipStream_t s) {
-    const int nbw = blocks_per_wave(P.hidden / 128);
+    const FusedShape f = fused_shape(P.hidden / 128);
     if constexpr (M == 1) {
-        const FusedShape f = fused_shape(P.hidden / 128);
         ev_before(EV_GATEUP, s);
         if (f.nb == 7) launch_fused<M, NG, 7, HZ>(P, f.waves, s);
         else launch_fused<M, NG, 8, HZ>(P, f.waves, s);
@@ -1195,8 +1198,8 @@ static void launch_compute(const DecodeParams& P, hipStream_t s) {
         return;
     }
     ev_before(EV_GATEUP, s);
-    if (nbw == 16) launch_gateup<M, NG, 1, 16, HZ>(P, s);
-    else launch_gateup<M, NG, 1, 8, HZ>(P, s);
+    if (f.nb == 7) launch_gateup<M, NG, 1, 7, HZ>(P, f.waves, s);
+    else launch_gateup<M, NG, 1, 8, HZ>(P, f.waves, s);
     ev_after(EV_GATEUP, s);
     ev_before(EV_DOWN, s);
     launch_down<M, NG, HZ>(P, s);
@@ -1262,7 +1265,7 @@ static hipError_t decode_run(const void* const* d_expert_table, const void* d_sh
     P.xh = x_direct ? (const uint16_t*)d_x : P.xconv;
     P.hperm = (uint16_t*)(ws + w.hperm);
     P.part = (float*)(ws + w.part);
-    P.gsplit = M == 1 ? fused_shape(P.hidden / 128).gsplit : 1;
+    P.gsplit = fused_shape(P.hidden / 128).gsplit;
     P.gcnt = (int*)(ws + w.gcnt);
     P.gpart = (float*)(ws + w.gpart);
     P.out32 = d_out_f32;
