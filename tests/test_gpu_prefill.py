@@ -136,6 +136,20 @@ def test_dsv3_shape_zipf():
                 check_tokens=[0, 1, 47, 95])
 
 
+@pytest.mark.parametrize("gs,zeros", [(64, False), (128, True), (32, False)])
+def test_long_k_scales_loaded_per_step(gs, zeros):
+    """Hidden 7168 with group size 64, zeros, or group size 32: the gate/up
+    scale (and zero) image of a workgroup exceeds the LDS budget, so the
+    kernels load scales per K step; the down projection (K = 256) stages
+    them in LDS."""
+    print(f"prefill long K gs={gs} zeros={zeros}", flush=True)
+    rng = np.random.default_rng(700 + gs)
+    T, n_exp, k = 48, 8, 2
+    idx = synth.zipf_topk(rng, T, n_exp, k)
+    w = synth.route_weights(rng, T, k)
+    run_prefill(700 + gs, 256, 7168, gs, n_exp, idx, w, True, zeros, check_tokens=[0, 17, 47])
+
+
 def test_matches_decode_path():
     """Every token of a 64-token prefill against the decode entry point run
     4 tokens at a time (itself checked against the oracle)."""

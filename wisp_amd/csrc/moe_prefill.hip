@@ -41,6 +41,8 @@
 #define PF_AROW 136               /* LDS A row stride in halves (128 + 8)    */
 #define PF_MAX_EXPERTS 4096
 #define PF_CLASSES 3              /* tiles of <= 32, <= 64, <= 128 tokens    */
+#define PF_SCALE_LDS_MAX 40960    /* byte budget of the LDS scale (and zero) image */
+#define PF_SCALE_PIECES 4         /* 16-byte scale pieces per lane and row tile when staged */
 
 struct PfParams {
     uint64_t p_off[3], s_off[3], z_off[3];
@@ -191,10 +193,11 @@ __device__ __forceinline__ uint32_t dequant2(uint32_t d, h2 s2, h2 z2) {
  * e0 e4 e1 e5 e2 e6 e3 e7. OR-ing a nibble into the mantissa of 1024.0
  * (0x6400) gives exactly 1024 + q. Written with one scalar per dword: an
  * element of a vector value subscripted by an unrolled loop index inside
- * __builtin_bit_cast was folded to element 0 by this compiler. */
+ * __builtin_bit_cast was folded to element 0 by this compiler. m =
+ * 0x000F000F and one024 = 0x64006400 come in VGPRs (see pf_gemm_kernel), so
+ * each and-or is one v_and_or_b32 (two literal operands would split it). */
 template <bool HZ>
-__device__ __forceinline__ h8 dequant8(uint32_t w, h2 s2, h2 z2) {
-    const uint32_t m = 0x000F000Fu, one024 = 0x64006400u;
+__device__ __forceinline__ h8 dequant8(uint32_t w, h2 s2, h2 z2, uint32_t m, uint32_t one024) {
     u4 o;
     o.x = dequant2<HZ>((w & m) | one024, s2, z2);
     o.y = dequant2<HZ>(((w >> 4) & m) | one024, s2, z2);
@@ -217,8 +220,15 @@ __device__ __forceinline__ h8 dequant8(uint32_t w, h2 s2, h2 z2) {
  *
  * Pipeline of step b: commit the A tile of block b + 1 (loaded during step
  * b - 1) to the other LDS buffer, issue the A loads of block b + 2, issue
- * the weights of block b + R - 1, compute block b, barrier. */
-template <bool GATEUP, bool HZ, int TV, int R, int WV>
+ * the weights of block b + R - 1, compute block b, barrier.
+ *
+ * SS: each wave first copies the scales (and zeros) of its row tiles for
+ * the whole K axis into dynamic LDS, [WV][NT][16][G] (16 consecutive rows
+ * are one contiguous run, copied with 16-byte loads), and the K loop reads
+ * them from there. Otherwise every step loads one 2-byte scale per lane and
+ * row tile, 16 rows and so 16 memory transactions per instruction: 18 % of
+ * the DeepSeek-V3 prefill layer on MI355X. */
+template <bool GATEUP, bool HZ, int TV, int R, int WV, bool SS>
 __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int cls) {
     constexpr int THREADS = 64 * WV;
     constexpr int NT = 16 / WV;                  /* 16-row weight tiles per wave */
@@ -228,6 +238,7 @@ __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int 
     __shared__ __attribute__((aligned(16))) uint16_t s_a[2][BM * PF_AROW];
     __shared__ int s_row[BM];      /* source row of each tile row (-1: none) */
     __shared__ float s_wr[BM];     /* routing weight of each tile row        */
+    extern __shared__ __attribute__((aligned(16))) uint16_t s_scl[];   /* SS image */
     const int tile = blockIdx.x;
     const int n_tiles = P.n_tiles[cls];
     const int4 td = P.tiles[cls * P.max_tiles + tile];
@@ -271,6 +282,36 @@ __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int 
     }
     /* group of this lane's 32 K values in block b: (128 b + 32 j) / gs */
     const int gshift = 31 - __builtin_clz(P.gs);
+    /* this wave's scale (zero) image: row tile s, row col at
+     * s_sc[(s * 16 + col) * G] (s_zc likewise) */
+    uint16_t* const s_sc = s_scl + (size_t)wave * NT * 16 * G;
+    uint16_t* const s_zc = s_scl + (size_t)(WV + wave) * NT * 16 * G;
+    if (SS) {
+        /* 16 rows x G fp16 = 2 G pieces of 16 B per row tile; all loads
+         * first, then the LDS writes (the weights come after) */
+        u4 sv[NT][PF_SCALE_PIECES], zv[NT][PF_SCALE_PIECES];
+#pragma unroll
+        for (int s = 0; s < NT; s++) {
+            const uint16_t* sb = sp[s] - (size_t)col * G;   /* the tile's first row */
+            const uint16_t* zb = zp[s] - (size_t)col * G;
+#pragma unroll
+            for (int c = 0; c < PF_SCALE_PIECES; c++) {
+                const int q = min(lane + 64 * c, 2 * G - 1);
+                sv[s][c] = *(const u4*)(sb + 8 * q);
+                if (HZ) zv[s][c] = *(const u4*)(zb + 8 * q);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < NT; s++)
+#pragma unroll
+            for (int c = 0; c < PF_SCALE_PIECES; c++) {
+                const int q = lane + 64 * c;
+                if (q < 2 * G) {
+                    *(u4*)(s_sc + s * 16 * G + 8 * q) = sv[s][c];
+                    if (HZ) *(u4*)(s_zc + s * 16 * G + 8 * q) = zv[s][c];
+                }
+            }
+    }
 
     f4 acc[TV][NT];
 #pragma unroll
@@ -313,10 +354,19 @@ __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int 
 #pragma unroll
         for (int s = 0; s < NT; s++) {
             wr[slot][s] = *(const u4*)(wp[s] + (size_t)bb * 64);
-            sr[slot][s] = sp[s][g];
-            if (HZ) zr[slot][s] = zp[s][g];
+            if (!SS) {
+                sr[slot][s] = sp[s][g];
+                if (HZ) zr[slot][s] = zp[s][g];
+            }
         }
     };
+
+    /* unpack constants pinned to VGPRs (an empty asm emits nothing): a VALU
+     * op takes at most one literal, so with literal masks every and-or of
+     * the dequant became a v_and_b32 plus a v_or_b32 */
+    uint32_t nib_mask = 0x000F000Fu, nib_one = 0x64006400u;
+    asm volatile("" : "+v"(nib_mask));
+    asm volatile("" : "+v"(nib_one));
 
     a_issue(0);
     a_commit(0);
@@ -334,6 +384,14 @@ __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int 
                 if (b + 2 < nblk) a_issue(b + 2);
                 w_issue((r + R - 1) % R, b + R - 1);
                 const uint16_t* abuf = &s_a[b & 1][0];
+                if (SS) {
+                    const int g = (b * 128 + 32 * j) >> gshift;
+#pragma unroll
+                    for (int s = 0; s < NT; s++) {
+                        sr[r][s] = s_sc[(s * 16 + col) * G + g];
+                        if (HZ) zr[r][s] = s_zc[(s * 16 + col) * G + g];
+                    }
+                }
 #pragma unroll
                 for (int kk = 0; kk < 4; kk++) {
                     h8 af[TV];
@@ -344,7 +402,8 @@ __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int 
                     for (int s = 0; s < NT; s++) {
                         const f16 sc = __builtin_bit_cast(f16, sr[r][s]);
                         const f16 zc = HZ ? __builtin_bit_cast(f16, zr[r][s]) : (f16)0.0f;
-                        const h8 bf = dequant8<HZ>(wr[r][s][kk], (h2){sc, sc}, (h2){zc, zc});
+                        const h8 bf = dequant8<HZ>(wr[r][s][kk], (h2){sc, sc}, (h2){zc, zc},
+                                                   nib_mask, nib_one);
 #pragma unroll
                         for (int t = 0; t < TV; t++) acc[t][s] = mfma16x16x32(af[t], bf, acc[t][s]);
                     }
@@ -467,15 +526,30 @@ extern "C" size_t wisp_moe_prefill_workspace_bytes(const WispExpertLayout* L, in
 /* One launch per tile class (sub-tiles per tile 2 / 4 / 8), each with its
  * own register budget; eight waves and a ring of four weight blocks measured
  * best for every class on MI355X (deeper rings cost occupancy). */
+template <bool GATEUP, bool HZ, bool SS>
+static void pf_launch_ss(const PfParams& P, const int* gx, size_t lds, hipStream_t s) {
+    const int ny = GATEUP ? P.inter / 128 : P.hidden / 256;
+    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 8, PF_RING, PF_WAVES, SS>), dim3(gx[2], ny),
+                       dim3(64 * PF_WAVES), lds, s, P, 2);
+    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 4, PF_RING, PF_WAVES, SS>), dim3(gx[1], ny),
+                       dim3(64 * PF_WAVES), lds, s, P, 1);
+    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 2, PF_RING, PF_WAVES, SS>), dim3(gx[0], ny),
+                       dim3(64 * PF_WAVES), lds, s, P, 0);
+}
+
+/* Scales (and zeros) staged in LDS when the image fits PF_SCALE_LDS_MAX and
+ * PF_SCALE_PIECES pieces per lane (DeepSeek-V3 gate/up at group size 128:
+ * 28 KiB); otherwise loaded per step. */
 template <bool GATEUP, bool HZ>
 static void pf_launch(const PfParams& P, const int* gx, hipStream_t s) {
-    const int ny = GATEUP ? P.inter / 128 : P.hidden / 256;
-    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 8, PF_RING, PF_WAVES>), dim3(gx[2], ny),
-                       dim3(64 * PF_WAVES), 0, s, P, 2);
-    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 4, PF_RING, PF_WAVES>), dim3(gx[1], ny),
-                       dim3(64 * PF_WAVES), 0, s, P, 1);
-    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 2, PF_RING, PF_WAVES>), dim3(gx[0], ny),
-                       dim3(64 * PF_WAVES), 0, s, P, 0);
+    const int K = GATEUP ? P.hidden : P.inter;
+    const int G = K / P.gs;
+    const int nt = 16 / PF_WAVES;
+    const size_t lds = (size_t)PF_WAVES * nt * 16 * G * 2 * (HZ ? 2 : 1);
+    if (lds <= PF_SCALE_LDS_MAX && 2 * G <= 64 * PF_SCALE_PIECES)
+        pf_launch_ss<GATEUP, HZ, true>(P, gx, lds, s);
+    else
+        pf_launch_ss<GATEUP, HZ, false>(P, gx, 0, s);
 }
 
 extern "C" hipError_t wisp_gpu_expert_offsets(const int* d_topk_idx, int n_tokens, int top_k,
