@@ -38,6 +38,7 @@
 #define PF_BM 128                 /* tokens per tile                         */
 #define PF_WAVES 8                /* waves per workgroup (NT = 2 row tiles each) */
 #define PF_RING 4                 /* weight blocks in the register ring (3 in flight) */
+#define PF_NT 2                   /* row tiles of 16 weight rows per wave        */
 #define PF_AROW 136               /* LDS A row stride in halves (128 + 8)    */
 #define PF_MAX_EXPERTS 4096
 #define PF_CLASSES 3              /* tiles of <= 32, <= 64, <= 128 tokens    */
@@ -206,12 +207,12 @@ __device__ __forceinline__ h8 dequant8(uint32_t w, h2 s2, h2 z2, uint32_t m, uin
     return __builtin_bit_cast(h8, o);
 }
 
-/* grid (tiles of class CLS, n-blocks); WV waves, each owning NT = 16 / WV
- * row tiles of 16 weight rows. GATEUP: the workgroup covers h features
- * [128 by, 128 by + 128): wave w owns gate rows f0 .. f0 + 8 NT - 1 and the
- * same up rows, f0 = 128 by + (128 / WV) w (row tiles s < NT/2 gate, the
- * rest up). DOWN: output rows [256 by, +256): wave w owns NT row tiles from
- * 256 by + (256 / WV) w. K = hidden (GATEUP) or inter (DOWN) in 128-wide
+/* grid (tiles of class CLS, n-blocks); WV waves, each owning NT row tiles
+ * of 16 weight rows. GATEUP: the workgroup covers FEAT = 8 NT WV h features
+ * [FEAT by, FEAT by + FEAT): wave w owns gate rows f0 .. f0 + 8 NT - 1 and
+ * the same up rows, f0 = FEAT by + 8 NT w (row tiles s < NT/2 gate, the
+ * rest up). DOWN: output rows [DROWS by, +DROWS), DROWS = 16 NT WV: wave w
+ * owns NT row tiles from DROWS by + 16 NT w. K = hidden (GATEUP) or inter (DOWN) in 128-wide
  * blocks. TV: 16-token sub-tiles of the class (rows past the tile's count
  * are zeros); R: weight blocks held in the register ring (R - 1 in flight
  * while one is computed). Eight waves with half the rows each halve the
@@ -228,10 +229,11 @@ __device__ __forceinline__ h8 dequant8(uint32_t w, h2 s2, h2 z2, uint32_t m, uin
  * them from there. Otherwise every step loads one 2-byte scale per lane and
  * row tile, 16 rows and so 16 memory transactions per instruction: 18 % of
  * the DeepSeek-V3 prefill layer on MI355X. */
-template <bool GATEUP, bool HZ, int TV, int R, int WV, bool SS>
+template <bool GATEUP, bool HZ, int TV, int R, int WV, bool SS, int NT>
 __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int cls) {
     constexpr int THREADS = 64 * WV;
-    constexpr int NT = 16 / WV;                  /* 16-row weight tiles per wave */
+    constexpr int FEAT = 8 * NT * WV;            /* gate/up: h features per workgroup */
+    constexpr int DROWS = 16 * NT * WV;          /* down: output rows per workgroup */
     constexpr int BM = 16 * TV;
     constexpr int APT = BM * 16 / THREADS;       /* A pieces (16 B) per thread per block */
     static_assert(APT >= 1 && APT * THREADS == BM * 16, "A staging must divide evenly");
@@ -271,10 +273,10 @@ __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int 
         int mat, row;
         if (GATEUP) {
             mat = s < NT / 2 ? 0 : 1;
-            row = blockIdx.y * 128 + wave * (128 / WV) + 16 * (s % (NT / 2)) + col;
+            row = blockIdx.y * FEAT + wave * (FEAT / WV) + 16 * (s % (NT / 2)) + col;
         } else {
             mat = 2;
-            row = blockIdx.y * 256 + wave * (256 / WV) + 16 * s + col;
+            row = blockIdx.y * DROWS + wave * (DROWS / WV) + 16 * s + col;
         }
         wp[s] = blob + P.p_off[mat] + (size_t)row * (K / 2) + 16 * j;
         sp[s] = (const uint16_t*)(blob + P.s_off[mat]) + (size_t)row * G;
@@ -426,13 +428,13 @@ __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int 
                     for (int s = 0; s < NT / 2; s++) {
                         const float g = acc[t][s][v], u = acc[t][NT / 2 + s][v];
                         const float h = silu_f(g) * u * wrt;
-                        const int c = blockIdx.y * 128 + wave * (128 / WV) + 16 * s + col;
+                        const int c = blockIdx.y * FEAT + wave * (FEAT / WV) + 16 * s + col;
                         P.H[(size_t)(p0 + r) * P.inter + c] = __builtin_bit_cast(uint16_t, (f16)h);
                     }
                 } else {
 #pragma unroll
                     for (int s = 0; s < NT; s++) {
-                        const int c = blockIdx.y * 256 + wave * (256 / WV) + 16 * s + col;
+                        const int c = blockIdx.y * DROWS + wave * (DROWS / WV) + 16 * s + col;
                         P.Y[(size_t)(p0 + r) * P.hidden + c] =
                             __builtin_bit_cast(uint16_t, (f16)acc[t][s][v]);
                     }
@@ -526,30 +528,35 @@ extern "C" size_t wisp_moe_prefill_workspace_bytes(const WispExpertLayout* L, in
 /* One launch per tile class (sub-tiles per tile 2 / 4 / 8), each with its
  * own register budget; eight waves and a ring of four weight blocks measured
  * best for every class on MI355X (deeper rings cost occupancy). */
-template <bool GATEUP, bool HZ, bool SS>
-static void pf_launch_ss(const PfParams& P, const int* gx, size_t lds, hipStream_t s) {
-    const int ny = GATEUP ? P.inter / 128 : P.hidden / 256;
-    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 8, PF_RING, PF_WAVES, SS>), dim3(gx[2], ny),
-                       dim3(64 * PF_WAVES), lds, s, P, 2);
-    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 4, PF_RING, PF_WAVES, SS>), dim3(gx[1], ny),
-                       dim3(64 * PF_WAVES), lds, s, P, 1);
-    hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, 2, PF_RING, PF_WAVES, SS>), dim3(gx[0], ny),
-                       dim3(64 * PF_WAVES), lds, s, P, 0);
-}
-
-/* Scales (and zeros) staged in LDS when the image fits PF_SCALE_LDS_MAX and
- * PF_SCALE_PIECES pieces per lane (DeepSeek-V3 gate/up at group size 128:
- * 28 KiB); otherwise loaded per step. */
-template <bool GATEUP, bool HZ>
-static void pf_launch(const PfParams& P, const int* gx, hipStream_t s) {
+/* One class: scales (and zeros) staged in LDS when the image fits `budget`
+ * and PF_SCALE_PIECES pieces per lane, else loaded per step. */
+template <bool GATEUP, bool HZ, int TV, int R, int WV, int NT>
+static void pf_launch_one(const PfParams& P, int gx, int cls, size_t budget, hipStream_t s) {
     const int K = GATEUP ? P.hidden : P.inter;
     const int G = K / P.gs;
-    const int nt = 16 / PF_WAVES;
-    const size_t lds = (size_t)PF_WAVES * nt * 16 * G * 2 * (HZ ? 2 : 1);
-    if (lds <= PF_SCALE_LDS_MAX && 2 * G <= 64 * PF_SCALE_PIECES)
-        pf_launch_ss<GATEUP, HZ, true>(P, gx, lds, s);
-    else
-        pf_launch_ss<GATEUP, HZ, false>(P, gx, 0, s);
+    const size_t lds = (size_t)WV * NT * 16 * G * 2 * (HZ ? 2 : 1);
+    const int ny = GATEUP ? P.inter / (8 * NT * WV) : P.hidden / (16 * NT * WV);
+    if (lds <= budget && 2 * G <= 64 * PF_SCALE_PIECES) {
+        auto k = pf_gemm_kernel<GATEUP, HZ, TV, R, WV, true, NT>;
+        if (lds > 65536)
+            (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)lds);
+        hipLaunchKernelGGL(k, dim3(gx, ny), dim3(64 * WV), lds, s, P, cls);
+    } else {
+        hipLaunchKernelGGL((pf_gemm_kernel<GATEUP, HZ, TV, R, WV, false, NT>), dim3(gx, ny),
+                           dim3(64 * WV), 0, s, P, cls);
+    }
+}
+
+/* Eight waves of 2 row tiles and a ring of four weight blocks for every
+ * class (measured on MI355X: 4 row tiles per wave, in 8-wave workgroups for
+ * the small classes or in 4-wave workgroups with accumulators in AGPRs for
+ * the full tiles, were slower: fewer workgroups per CU). */
+template <bool GATEUP, bool HZ>
+static void pf_launch(const PfParams& P, const int* gx, hipStream_t s) {
+    pf_launch_one<GATEUP, HZ, 8, PF_RING, PF_WAVES, PF_NT>(P, gx[2], 2, PF_SCALE_LDS_MAX, s);
+    pf_launch_one<GATEUP, HZ, 4, PF_RING, PF_WAVES, PF_NT>(P, gx[1], 1, PF_SCALE_LDS_MAX, s);
+    pf_launch_one<GATEUP, HZ, 2, PF_RING, PF_WAVES, PF_NT>(P, gx[0], 0, PF_SCALE_LDS_MAX, s);
 }
 
 extern "C" hipError_t wisp_gpu_expert_offsets(const int* d_topk_idx, int n_tokens, int top_k,
