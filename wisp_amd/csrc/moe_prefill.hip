@@ -39,6 +39,7 @@
 #define PF_WAVES 8                /* waves per workgroup (NT = 2 row tiles each) */
 #define PF_RING 4                 /* weight blocks in the register ring (3 in flight) */
 #define PF_NT 2                   /* row tiles of 16 weight rows per wave        */
+#define PF_XCDS 8                 /* accelerator dies: workgroups are dealt to them round-robin */
 #define PF_AROW 136               /* LDS A row stride in halves (128 + 8)    */
 #define PF_MAX_EXPERTS 4096
 #define PF_CLASSES 3              /* tiles of <= 32, <= 64, <= 128 tokens    */
@@ -241,10 +242,20 @@ __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int 
     __shared__ int s_row[BM];      /* source row of each tile row (-1: none) */
     __shared__ float s_wr[BM];     /* routing weight of each tile row        */
     extern __shared__ __attribute__((aligned(16))) uint16_t s_scl[];   /* SS image */
-    const int tile = blockIdx.x;
+    /* XCD-aware order: the hardware deals workgroups to the PF_XCDS dies
+     * round-robin by linear id (x fastest), and each die has its own L2.
+     * Die d's k-th workgroup takes tile 8 (k / ny) + d, n-block k % ny, so
+     * all n-blocks of a tile run together on one die and its gathered
+     * token rows come from that die's L2 after the first read (gridDim.x
+     * is a multiple of PF_XCDS). */
+    const int ny = gridDim.y;
+    const int lin = blockIdx.x + gridDim.x * blockIdx.y;
+    const int slot = lin / PF_XCDS;
+    const int tile = (slot / ny) * PF_XCDS + lin % PF_XCDS;
+    const int by = slot % ny;
     const int n_tiles = P.n_tiles[cls];
-    const int4 td = P.tiles[cls * P.max_tiles + tile];
     if (tile >= n_tiles) return;
+    const int4 td = P.tiles[cls * P.max_tiles + tile];
     const int e = td.x, p0 = td.y, nv = td.z;
     const uint8_t* blob = P.table1[e];
     const int K = GATEUP ? P.hidden : P.inter;
@@ -273,10 +284,10 @@ __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int 
         int mat, row;
         if (GATEUP) {
             mat = s < NT / 2 ? 0 : 1;
-            row = blockIdx.y * FEAT + wave * (FEAT / WV) + 16 * (s % (NT / 2)) + col;
+            row = by * FEAT + wave * (FEAT / WV) + 16 * (s % (NT / 2)) + col;
         } else {
             mat = 2;
-            row = blockIdx.y * DROWS + wave * (DROWS / WV) + 16 * s + col;
+            row = by * DROWS + wave * (DROWS / WV) + 16 * s + col;
         }
         wp[s] = blob + P.p_off[mat] + (size_t)row * (K / 2) + 16 * j;
         sp[s] = (const uint16_t*)(blob + P.s_off[mat]) + (size_t)row * G;
@@ -428,13 +439,13 @@ __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int 
                     for (int s = 0; s < NT / 2; s++) {
                         const float g = acc[t][s][v], u = acc[t][NT / 2 + s][v];
                         const float h = silu_f(g) * u * wrt;
-                        const int c = blockIdx.y * FEAT + wave * (FEAT / WV) + 16 * s + col;
+                        const int c = by * FEAT + wave * (FEAT / WV) + 16 * s + col;
                         P.H[(size_t)(p0 + r) * P.inter + c] = __builtin_bit_cast(uint16_t, (f16)h);
                     }
                 } else {
 #pragma unroll
                     for (int s = 0; s < NT; s++) {
-                        const int c = blockIdx.y * DROWS + wave * (DROWS / WV) + 16 * s + col;
+                        const int c = by * DROWS + wave * (DROWS / WV) + 16 * s + col;
                         P.Y[(size_t)(p0 + r) * P.hidden + c] =
                             __builtin_bit_cast(uint16_t, (f16)acc[t][s][v]);
                     }
@@ -627,7 +638,10 @@ extern "C" hipError_t wisp_gpu_moe_prefill_int4(const void* const* d_expert_tabl
     /* grid.x per class: an upper bound on its tile count */
     const int np = n_tokens * P.top_k1;
     int gx[PF_CLASSES] = {P.n_experts1, np / 33 + P.n_experts1, np / 65 + P.n_experts1};
-    for (int k = 0; k < PF_CLASSES; k++) gx[k] = gx[k] < P.max_tiles ? gx[k] : P.max_tiles;
+    for (int k = 0; k < PF_CLASSES; k++) {
+        gx[k] = gx[k] < P.max_tiles ? gx[k] : P.max_tiles;
+        gx[k] = (gx[k] + PF_XCDS - 1) / PF_XCDS * PF_XCDS;   /* whole dies (XCD-aware order) */
+    }
     ev_before(EV_PF_GATEUP, s);
     if (hz) pf_launch<true, true>(P, gx, s);
     else pf_launch<true, false>(P, gx, s);
