@@ -44,6 +44,7 @@
 #define PF_MAX_EXPERTS 4096
 #define PF_CLASSES 3              /* tiles of <= 32, <= 64, <= 128 tokens    */
 #define PF_SCALE_LDS_MAX 40960    /* byte budget of the LDS scale (and zero) image */
+#define PF_SCALE_LDS_WIDE 65536   /* the same for the wide full-tile kernel      */
 #define PF_SCALE_PIECES 4         /* 16-byte scale pieces per lane and row tile when staged */
 
 struct PfParams {
@@ -407,18 +408,39 @@ __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int 
                 }
 #pragma unroll
                 for (int kk = 0; kk < 4; kk++) {
-                    h8 af[TV];
+                    if constexpr (NT > 2) {
+                        /* wide waves: the NT weight fragments first, then one
+                         * activation fragment at a time (registers) */
+                        h8 bf[NT];
 #pragma unroll
-                    for (int t = 0; t < TV; t++)
-                        af[t] = *(const h8*)(abuf + (16 * t + col) * PF_AROW + 32 * j + 8 * kk);
+                        for (int s = 0; s < NT; s++) {
+                            const f16 sc = __builtin_bit_cast(f16, sr[r][s]);
+                            const f16 zc = HZ ? __builtin_bit_cast(f16, zr[r][s]) : (f16)0.0f;
+                            bf[s] = dequant8<HZ>(wr[r][s][kk], (h2){sc, sc}, (h2){zc, zc},
+                                                 nib_mask, nib_one);
+                        }
 #pragma unroll
-                    for (int s = 0; s < NT; s++) {
-                        const f16 sc = __builtin_bit_cast(f16, sr[r][s]);
-                        const f16 zc = HZ ? __builtin_bit_cast(f16, zr[r][s]) : (f16)0.0f;
-                        const h8 bf = dequant8<HZ>(wr[r][s][kk], (h2){sc, sc}, (h2){zc, zc},
-                                                   nib_mask, nib_one);
+                        for (int t = 0; t < TV; t++) {
+                            const h8 af = *(const h8*)(abuf + (16 * t + col) * PF_AROW + 32 * j + 8 * kk);
 #pragma unroll
-                        for (int t = 0; t < TV; t++) acc[t][s] = mfma16x16x32(af[t], bf, acc[t][s]);
+                            for (int s = 0; s < NT; s++) acc[t][s] = mfma16x16x32(af, bf[s], acc[t][s]);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    } else {
+                        h8 af[TV];
+#pragma unroll
+                        for (int t = 0; t < TV; t++)
+                            af[t] = *(const h8*)(abuf + (16 * t + col) * PF_AROW + 32 * j + 8 * kk);
+#pragma unroll
+                        for (int s = 0; s < NT; s++) {
+                            const f16 sc = __builtin_bit_cast(f16, sr[r][s]);
+                            const f16 zc = HZ ? __builtin_bit_cast(f16, zr[r][s]) : (f16)0.0f;
+                            const h8 bf = dequant8<HZ>(wr[r][s][kk], (h2){sc, sc}, (h2){zc, zc},
+                                                       nib_mask, nib_one);
+#pragma unroll
+                            for (int t = 0; t < TV; t++)
+                                acc[t][s] = mfma16x16x32(af[t], bf, acc[t][s]);
+                        }
                     }
                 }
                 __syncthreads();
@@ -559,13 +581,41 @@ static void pf_launch_one(const PfParams& P, int gx, int cls, size_t budget, hip
     }
 }
 
-/* Eight waves of 2 row tiles and a ring of four weight blocks for every
- * class (measured on MI355X: 4 row tiles per wave, in 8-wave workgroups for
- * the small classes or in 4-wave workgroups with accumulators in AGPRs for
- * the full tiles, were slower: fewer workgroups per CU). */
+/* The full 128-token tiles without zero points: 4 row tiles per wave
+ * (256 h features or 512 output rows per workgroup, ring of 3), so each
+ * activation fragment read from LDS feeds 4 MFMAs instead of 2; it fits
+ * 256 VGPRs only with the scales in LDS and no zeros. Returns false when
+ * the shape or the scale image does not allow it. */
+template <bool GATEUP, bool HZ>
+static bool pf_launch_wide(const PfParams& P, int gx, hipStream_t s) {
+    if constexpr (HZ) {
+        return false;
+    } else {
+        constexpr int NTW = 4;
+        const int K = GATEUP ? P.hidden : P.inter;
+        const int G = K / P.gs;
+        const size_t lds = (size_t)PF_WAVES * NTW * 16 * G * 2;
+        if (P.inter % (8 * NTW * PF_WAVES) || P.hidden % (16 * NTW * PF_WAVES) ||
+            lds > PF_SCALE_LDS_WIDE || 2 * G > 64 * PF_SCALE_PIECES)
+            return false;
+        auto k = pf_gemm_kernel<GATEUP, false, 8, 3, PF_WAVES, true, NTW>;
+        if (lds > 65536)
+            (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)lds);
+        const int ny = GATEUP ? P.inter / (8 * NTW * PF_WAVES) : P.hidden / (16 * NTW * PF_WAVES);
+        hipLaunchKernelGGL(k, dim3(gx, ny), dim3(64 * PF_WAVES), lds, s, P, 2);
+        return true;
+    }
+}
+
+/* Eight waves of 2 row tiles and a ring of four weight blocks for the other
+ * tiles (measured on MI355X: 4 row tiles per wave for the small classes cost
+ * a workgroup per CU and were slower, as were 4-wave workgroups with
+ * accumulators in AGPRs for the full tiles). */
 template <bool GATEUP, bool HZ>
 static void pf_launch(const PfParams& P, const int* gx, hipStream_t s) {
-    pf_launch_one<GATEUP, HZ, 8, PF_RING, PF_WAVES, PF_NT>(P, gx[2], 2, PF_SCALE_LDS_MAX, s);
+    if (!pf_launch_wide<GATEUP, HZ>(P, gx[2], s))
+        pf_launch_one<GATEUP, HZ, 8, PF_RING, PF_WAVES, PF_NT>(P, gx[2], 2, PF_SCALE_LDS_MAX, s);
     pf_launch_one<GATEUP, HZ, 4, PF_RING, PF_WAVES, PF_NT>(P, gx[1], 1, PF_SCALE_LDS_MAX, s);
     pf_launch_one<GATEUP, HZ, 2, PF_RING, PF_WAVES, PF_NT>(P, gx[0], 0, PF_SCALE_LDS_MAX, s);
 }
