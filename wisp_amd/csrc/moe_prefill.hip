@@ -617,7 +617,9 @@ static void pf_launch(const PfParams& P, const int* gx, hipStream_t s) {
     if (!pf_launch_wide<GATEUP, HZ>(P, gx[2], s))
         pf_launch_one<GATEUP, HZ, 8, PF_RING, PF_WAVES, PF_NT>(P, gx[2], 2, PF_SCALE_LDS_MAX, s);
     pf_launch_one<GATEUP, HZ, 4, PF_RING, PF_WAVES, PF_NT>(P, gx[1], 1, PF_SCALE_LDS_MAX, s);
-    pf_launch_one<GATEUP, HZ, 2, PF_RING, PF_WAVES, PF_NT>(P, gx[0], 0, PF_SCALE_LDS_MAX, s);
+    /* ring of 3 for the <= 32-token tiles: 79 VGPRs, 6 waves per SIMD (3
+     * workgroups per CU instead of 2), 1.5 % faster layer */
+    pf_launch_one<GATEUP, HZ, 2, 3, PF_WAVES, PF_NT>(P, gx[0], 0, PF_SCALE_LDS_MAX, s);
 }
 
 extern "C" hipError_t wisp_gpu_expert_offsets(const int* d_topk_idx, int n_tokens, int top_k,
