@@ -794,7 +794,8 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
     if (FUSED) {
         __builtin_amdgcn_s_waitcnt(0);   /* the wave's h' stores are acknowledged */
         if (lane == 0)
-            __hip_atomic_fetch_add(P.hcnt + (u * P.upe + r0 / (DEC_UNIT_BLOCKS * 128)) * DEC_HCNT_STRIDE, 1,
+            __hip_atomic_fetch_add(P.hcnt + (u * P.upe + r0 / (DEC_UNIT_BLOCKS * 128)) *
+                                                DEC_HCNT_STRIDE, 1,
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
@@ -1153,7 +1154,8 @@ static void launch_gateup(const DecodeParams& P, int waves, hipStream_t s) {
     const LdsMap L = lds_map(M, 2 * TILES, xk, P.hidden / P.gs, HZ, waves);
     auto k = gateup_kernel<M, NG, TILES, NB, HZ>;
     if (L.bytes > 65536)
-        (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, L.bytes);
+        (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  L.bytes);
     hipLaunchKernelGGL(k, dim3(P.inter / (16 * TILES) * P.gsplit, P.max_u), dim3(64 * waves),
                        L.bytes, s, P);
 }

@@ -214,7 +214,8 @@ __device__ __forceinline__ h8 dequant8(uint32_t w, h2 s2, h2 z2, uint32_t m, uin
  * [FEAT by, FEAT by + FEAT): wave w owns gate rows f0 .. f0 + 8 NT - 1 and
  * the same up rows, f0 = FEAT by + 8 NT w (row tiles s < NT/2 gate, the
  * rest up). DOWN: output rows [DROWS by, +DROWS), DROWS = 16 NT WV: wave w
- * owns NT row tiles from DROWS by + 16 NT w. K = hidden (GATEUP) or inter (DOWN) in 128-wide
+ * owns NT row tiles from DROWS by + 16 NT w. K = hidden (GATEUP) or inter
+ * (DOWN) in 128-wide
  * blocks. TV: 16-token sub-tiles of the class (rows past the tile's count
  * are zeros); R: weight blocks held in the register ring (R - 1 in flight
  * while one is computed). Eight waves with half the rows each halve the
@@ -248,7 +249,8 @@ __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int 
      * Die d's k-th workgroup takes tile 8 (k / ny) + d, n-block k % ny, so
      * all n-blocks of a tile run together on one die and its gathered
      * token rows come from that die's L2 after the first read (gridDim.x
-     * is a multiple of PF_XCDS). */
+     * is a multiple of PF_XCDS). The map is a bijection for any PF_XCDS;
+     * the die count only decides the locality. */
     const int ny = gridDim.y;
     const int lin = blockIdx.x + gridDim.x * blockIdx.y;
     const int slot = lin / PF_XCDS;
@@ -421,9 +423,11 @@ __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int 
                         }
 #pragma unroll
                         for (int t = 0; t < TV; t++) {
-                            const h8 af = *(const h8*)(abuf + (16 * t + col) * PF_AROW + 32 * j + 8 * kk);
+                            const h8 af =
+                                *(const h8*)(abuf + (16 * t + col) * PF_AROW + 32 * j + 8 * kk);
 #pragma unroll
-                            for (int s = 0; s < NT; s++) acc[t][s] = mfma16x16x32(af, bf[s], acc[t][s]);
+                            for (int s = 0; s < NT; s++)
+                                acc[t][s] = mfma16x16x32(af, bf[s], acc[t][s]);
                         }
                         __builtin_amdgcn_sched_barrier(0);
                     } else {
