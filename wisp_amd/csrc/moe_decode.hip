@@ -56,7 +56,8 @@
 #define DEC_UNIT_BLOCKS 8     /* down projection: 128-wide K blocks per wave unit */
 #define DN_WAVES 4            /* down projection: wave units per workgroup */
 #define DEC_HCNT_STRIDE 64    /* ints between wave-unit counters (own memory line each) */
-#define DEC_POLL_SLEEP 16     /* s_sleep units (64 cycles) between polls of a counter */
+#define DEC_POLL_SLEEP 8      /* s_sleep units (64 cycles) between polls of a counter (8: measured
+                                 0.2-0.5 us faster per layer than 16, 4 no better) */
 #define DEC_ROUTE_MAX_EXPERTS 1024
 #define DEC_PREP_THREADS 512
 
