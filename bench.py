@@ -470,7 +470,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the int4 MoE expert path here is a single-GPU "
-              "build (expert-parallel sharding is described in DESIGN.md, not run)", file=sys.stderr)
+              "build; expert-parallel sharding over several GPUs is not run", file=sys.stderr)
         sys.exit(2)
 
     from wisp_amd import synth

@@ -171,6 +171,16 @@ def test_one_token_64_experts_router_workgroups():
               vary_x=True)
 
 
+@pytest.mark.parametrize("n_exp,k,kind", [(5, 2, "softmax"), (12, 3, "sigmoid"),
+                                          (16, 4, "softmax"), (40, 6, "sigmoid")])
+def test_one_token_selection_expert_counts(n_exp, k, kind):
+    # the one-wave selection ranks against only the LDS keys in use (8, 16,
+    # 32 or 64 slots); expert counts inside and at the edge of each bound
+    print(f"layer M=1 one-wave selection E={n_exp} k={k} {kind}", flush=True)
+    run_layer(740 + n_exp, 256, 512, n_exp, k, 1, kind, shared=(n_exp % 2 == 0),
+              use_bias=(kind == "sigmoid"), repeat=2, vary_x=True)
+
+
 @pytest.mark.parametrize("n_exp", [32, 256])
 def test_sigmoid_nan_logit_never_selected(n_exp):
     # a NaN router row gives a NaN key: the oracle's "largest untaken" never

@@ -252,7 +252,11 @@ __device__ __forceinline__ void topk_wave_small(const float* lg, const uint16_t*
     const float inv = 1.0f / (denom > 0.0f ? denom : 1.0f);
     const float score = sig ? v : v * inv;
     if (act) scores_out[lane] = score;
-    const int rank = lds_rank<32>(s_key, ce);
+    /* keys past n_experts are 0 and never outrank: walk only the used pairs */
+    const int rank = n_experts <= 8    ? lds_rank<4>(s_key, ce)
+                     : n_experts <= 16 ? lds_rank<8>(s_key, ce)
+                     : n_experts <= 32 ? lds_rank<16>(s_key, ce)
+                                       : lds_rank<32>(s_key, ce);
     const bool picked = act && (ce >> 32) != 0 && rank < top_k;
     /* lane q takes the expert of rank q */
     if (lane < top_k) s_sel[lane] = -1;
