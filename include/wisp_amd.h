@@ -204,12 +204,31 @@ hipError_t wisp_gpu_moe_scatter(const float* d_y, const int* d_inv,
 
 enum { WISP_DTYPE_F16 = 0, WISP_DTYPE_F32 = 1 };
 
-/* Workspace bytes for wisp_gpu_moe_decode_int4. */
+/* Workspace bytes for wisp_gpu_moe_decode_int4. A decode workspace is
+ * dedicated to the decode entry points (it may be shared by calls of
+ * different shapes, one at a time): it carries a routing epoch and tagged
+ * routing words from call to call, so it must not be reused for anything
+ * else between them. It needs no zeroing, not even before its first use. */
 size_t wisp_moe_decode_workspace_bytes(const WispExpertLayout* L,
                                        int n_tokens, int top_k,
                                        int has_shared);
 
-/* d_expert_table: device array [n_experts] of device blob base pointers
+/* Bits of the decode status word. The decode kernels hand work from one
+ * workgroup to another through bounded waits (about 14 ms); a wait that
+ * gives up sets its bit and poisons the outputs it feeds with NaN. */
+enum {
+    WISP_DECODE_ROUTER_WAIT = 1,   /* router logits never reached the prep  */
+    WISP_DECODE_DOWN_WAIT = 2      /* a down projection never saw its h'    */
+};
+
+/* Waits for stream s, then returns in *flags the sticky status bits that
+ * decode calls on d_workspace have set since it was last cleared (0: every
+ * wait completed), and clears them when clear != 0. Synchronous. */
+hipError_t wisp_moe_decode_status(void* d_workspace, hipStream_t s,
+                                  uint32_t* flags, int clear);
+
+/* n_experts: 1..1024.
+ * d_expert_table: device array [n_experts] of device blob base pointers
  *   (each blob base at 8 mod 16, see wisp_expert_layout_check).
  * d_shared_blob: device blob of the always-on shared expert, or NULL.
  * d_x: [n_tokens, hidden], fp16 or fp32 per x_dtype.
@@ -348,7 +367,8 @@ void wisp_tier_policy_stats(const WispTierPolicy* t, uint64_t* out);
  * index l * n_experts + e, each blob_bytes long. Allocates n_slots +
  * scratch_slots device slots (blob at slot + 8, so that every section is
  * 16-byte aligned) and a device table [n_layers][n_experts] of blob
- * pointers. Returns NULL and sets *err on failure. */
+ * pointers. n_experts: 1..1024 (the decode kernels' limit). Returns NULL
+ * and sets *err on failure. */
 typedef struct WispExpertTier WispExpertTier;
 WispExpertTier* wisp_tier_create(int n_layers, int n_experts,
                                  size_t blob_bytes,

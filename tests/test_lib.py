@@ -100,6 +100,17 @@ def test_host_side_validation_rejects_without_gpu_calls():
     assert lib.wisp_gpu_moe_decode_int4(*args(0, ws)) == 1
     assert lib.wisp_gpu_moe_decode_int4(*args(5, ws)) == 1
     assert lib.wisp_gpu_moe_decode_int4(*args(1, ws - 1)) == 1
+    # more experts than the prep workgroup's LDS table holds (1024)
+    big = (fake, None, ctypes.byref(L), fake, 0, 1, fake, fake, 2, 1025, fake, 1 << 30, 0, fake,
+           None, None)
+    assert lib.wisp_gpu_moe_decode_int4(*big) == 1
+    assert lib.wisp_gpu_moe_layer_decode_int4(fake, None, 0, fake, fake, fake, fake, None,
+                                              ctypes.byref(L), fake, 0, 1, 2, 1025, fake, 1 << 30,
+                                              0, fake, None, None) == 1
+    err = ctypes.c_int(0)
+    ptrs = (ctypes.c_void_p * 1025)(*([fake] * 1025))
+    assert lib.wisp_tier_create(1, 1025, 4096, ptrs, 4, 10, 3, ctypes.byref(err)) is None
+    assert err.value == 1
     L.group_size = 48
     assert lib.wisp_gpu_moe_decode_int4(*args(1, 1 << 30)) == 1
     assert lib.wisp_gpu_moe_route(fake, None, fake, 1, 512, 2048, 8, 0, fake, fake, fake, None) == 1

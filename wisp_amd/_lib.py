@@ -52,6 +52,7 @@ _SIGS = {
     "wisp_gpu_moe_layer_decode_int4": (c_int, [P, P, c_int, P, P, P, P, P, POINTER(WispExpertLayout),
                                                P, c_int, c_int, c_int, c_int, P, c_size_t, c_int,
                                                P, P, P]),
+    "wisp_moe_decode_status": (c_int, [P, P, P, c_int]),
     # section 5: fused prefill
     "wisp_moe_prefill_workspace_bytes": (c_size_t, [POINTER(WispExpertLayout), c_int, c_int, c_int,
                                                     c_int]),
@@ -74,6 +75,8 @@ _SIGS = {
                                            P, P, c_int, P, c_size_t, P, P, P]),
     # profiling
     "wisp_amd_set_kernel_events": (None, [P, c_int]),
+    # internal test hook (not in the header): bounded-wait poll limit and target offset
+    "wisp_amd__test_decode_wait": (None, [c_int, c_int]),
     "wisp_amd_version": (c_char_p, []),
 }
 

@@ -43,6 +43,7 @@
 #include "../../include/wisp_amd.h"
 
 #define WISP_TIER_MAX_PAIRS 256   /* n_tokens * top_k of one decode layer (4 x 64) */
+#define WISP_TIER_MAX_EXPERTS 1024 /* experts per layer: the decode kernels' limit */
 
 namespace {
 
@@ -247,7 +248,8 @@ extern "C" WispExpertTier* wisp_tier_create(int n_layers, int n_experts, size_t 
     hipError_t e = hipErrorInvalidValue;
     WispExpertTier* t = nullptr;
     if (n_layers >= 1 && n_experts >= 1 && blob_bytes > 0 && host_blobs && n_slots >= 0 &&
-        scratch_slots >= 1 && promote_hits >= 1 && (long)n_layers * n_experts <= (1L << 24)) {
+        scratch_slots >= 1 && promote_hits >= 1 && n_experts <= WISP_TIER_MAX_EXPERTS &&
+        (long)n_layers * n_experts <= (1L << 24)) {
         t = new (std::nothrow) WispExpertTier(n_layers, n_experts, n_slots, scratch_slots,
                                               promote_hits);
         e = t ? hipSuccess : hipErrorOutOfMemory;

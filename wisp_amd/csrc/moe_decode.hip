@@ -85,6 +85,9 @@ struct DecodeParams {
     float* out32;         /* [M][hidden] layer output (either may be null) */
     uint16_t* out16;
     int accumulate;
+    uint32_t* status;     /* sticky DEC_STATUS_* bits of bounded waits that gave up */
+    int poll_limit;       /* polls of one hand-off word or counter before giving up */
+    int poll_extra;       /* added to every wait target: nonzero only to force a give-up */
 };
 
 /* Routing inputs of the prep kernel. mode 0: idx/w are given; mode 1: raw
@@ -130,9 +133,21 @@ static inline size_t prep_lds_bytes(int mode, int n_experts, int M) {
     return (size_t)prep_key_bytes(n_experts) + align_up_dev(M * n_experts * 4, 16);
 }
 
-/* Polls of one routing word before the prep workgroup gives up on it (about
- * 80 ms): the wait ends even if a router workgroup never ran. */
+/* Polls of one hand-off word or counter before a wait gives up: 65,536
+ * polls of 512 cycles each, about 14 ms at 2.4 GHz, so every wait ends even
+ * if the workgroup it waits for never ran. A wait that gives up sets its
+ * bit in the workspace's sticky status word (wisp_moe_decode_status reads
+ * and clears it) and poisons what it feeds with NaN, so a broken hand-off
+ * never passes for a result. */
 #define DEC_POLL_LIMIT (1 << 16)
+#define DEC_STATUS_ROUTER_WAIT 1u   /* prep: router logits never arrived  */
+#define DEC_STATUS_DOWN_WAIT 2u     /* down wave: h' of its unit never completed */
+/* Byte offset of the status word in every decode workspace. */
+#define DEC_STATUS_OFFSET 128
+
+__device__ __forceinline__ void dec_report(uint32_t* status, uint32_t bit) {
+    __hip_atomic_fetch_or(status, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 /* The prep workgroup has DEC_PREP_THREADS threads.
  *
@@ -255,6 +270,9 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
             P.xconv[i] = __builtin_bit_cast(uint16_t, (f16)xval<XT>(x, i));
     }
 
+    /* NaN when the routing wait gave up (multiplies every routing weight:
+     * x * 1 is exact, so it changes nothing otherwise) */
+    float poison = 1.0f;
     if (R.mode != 0) {
         /* dynamic LDS: 64-bit selection keys (scratch of the top-k), then
          * scores [M][n_experts] (the raw logits first) */
@@ -269,18 +287,24 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
             /* raw logits published by this launch's router workgroups */
             const uint32_t tok =
                 __hip_atomic_load(R.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+            const uint32_t want = tok + (uint32_t)P.poll_extra;
             int polls = 0;
+            bool gave_up = false;
             for (int i = threadIdx.x; i < M * n_experts; i += blockDim.x) {
                 uint64_t v = __hip_atomic_load(R.words + i, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT);
-                while ((uint32_t)(v >> 32) != tok && polls < DEC_POLL_LIMIT) {
+                while ((uint32_t)(v >> 32) != want && polls < P.poll_limit) {
                     __builtin_amdgcn_s_sleep(8);
                     polls++;
                     v = __hip_atomic_load(R.words + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
+                gave_up |= (uint32_t)(v >> 32) != want;
                 s_sc[i] = __uint_as_float((uint32_t)v);
             }
-            __syncthreads();
+            if (__syncthreads_or(gave_up)) {
+                poison = __builtin_nanf("");
+                if (threadIdx.x == 0) dec_report(P.status, DEC_STATUS_ROUTER_WAIT);
+            }
             if (threadIdx.x == 0)
                 __hip_atomic_store(R.epoch, tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -290,6 +314,7 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
             const int base = shared_blob ? 1 : 0;
             const bool valid = lane < top_k && e >= 0;
             const uint64_t m = __ballot(valid);
+            w *= poison;
             if (lane < top_k) {
                 R.idx[lane] = e;
                 R.w[lane] = w;
@@ -303,7 +328,7 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
                 *P.n_unique = base + __popcll(m);
                 if (shared_blob) {
                     P.ublob[0] = (const uint8_t*)shared_blob;
-                    for (int v = 0; v < DEC_MAX_TOKENS; v++) P.uw[v] = v == 0 ? 1.0f : 0.0f;
+                    for (int v = 0; v < DEC_MAX_TOKENS; v++) P.uw[v] = v == 0 ? poison : 0.0f;
                 }
             }
         };
@@ -364,7 +389,7 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     if (R.mode != 0) {
         for (int p = threadIdx.x; p < n_pairs; p += blockDim.x) {
             R.idx[p] = s_e[p];
-            R.w[p] = s_w[p];
+            R.w[p] = s_w[p] * poison;
         }
     }
 
@@ -394,7 +419,7 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
         float acc[DEC_MAX_TOKENS] = {0.f, 0.f, 0.f, 0.f};
         for (int q = p; q < n_pairs; q++)
             if (s_e[q] == e) acc[q / top_k] += s_w[q];
-        for (int v = 0; v < DEC_MAX_TOKENS; v++) P.uw[slot * 4 + v] = acc[v];
+        for (int v = 0; v < DEC_MAX_TOKENS; v++) P.uw[slot * 4 + v] = acc[v] * poison;
     }
     if (p == 0) {
         int total = base;
@@ -402,7 +427,7 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
         *P.n_unique = total;
         if (shared_blob) {
             P.ublob[0] = (const uint8_t*)shared_blob;
-            for (int v = 0; v < DEC_MAX_TOKENS; v++) P.uw[v] = v < M ? 1.0f : 0.0f;
+            for (int v = 0; v < DEC_MAX_TOKENS; v++) P.uw[v] = v < M ? poison : 0.0f;
         }
     }
 }
@@ -945,15 +970,18 @@ __device__ __forceinline__ void down_tile(const DecodeParams& P, int q, int rt, 
     const uint8_t* wp[1] = {blob + P.p_off[2] + (size_t)(r0 + col) * (K / 2) + 16 * j};
     u4 w[NB][1];
     load_blocks<1, NB>(wp, lb0, lb1 - 1, w);
+    bool gave_up = false;
     if (FUSED) {
         /* h' of this unit: written by nb * 8 gate/up workgroups */
+        const int want = nb * 8 + P.poll_extra;
         int polls = 0;
-        while (hc < nb * 8 && polls < DEC_POLL_LIMIT) {
+        while (hc < want && polls < P.poll_limit) {
             __builtin_amdgcn_s_sleep(DEC_POLL_SLEEP);
             polls++;
             hc = __hip_atomic_load(P.hcnt + gu * DEC_HCNT_STRIDE, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
         }
+        gave_up = hc < want;
         load_h();
     }
 
@@ -981,6 +1009,12 @@ __device__ __forceinline__ void down_tile(const DecodeParams& P, int q, int rt, 
     __builtin_amdgcn_wave_barrier();
     compute_blocks<M, NG, 1, NB, HZ>(w, smem, L, lb0, lb1, lb0, g_lo, P.gshift, col, j,
                                      P.m_lo, P.m_hi, P.one024, tot);
+    if (gave_up) {
+        /* the unit's h' may be stale: poison the row tile's sums */
+#pragma unroll
+        for (int v = 0; v < M; v++) tot[0][v] = __builtin_nanf("");
+        if (lane == 0) dec_report(P.status, DEC_STATUS_DOWN_WAIT);
+    }
     }
 
     float* red = (float*)(smem + L.red_off);
@@ -1116,12 +1150,18 @@ static FusedShape fused_shape(int nblk) {
     return f;
 }
 
+/* The first three regions sit at the same offsets for every layer shape,
+ * so one workspace can serve calls of different shapes: the unique count
+ * (offset 0) and the status word (DEC_STATUS_OFFSET), the routing epoch,
+ * and the routing words, which every call of any shape only ever tags with
+ * tokens up to the epoch. */
 static WsLayout ws_layout(const WispExpertLayout* L, int M, int top_k, int has_shared) {
     WsLayout w;
     w.max_u = (has_shared ? 1 : 0) + M * top_k;
     size_t off = 0;
     w.nu = off; off += 256;
     w.epoch = off; off += 256;
+    w.rwords = off; off += (size_t)DEC_MAX_TOKENS * DEC_ROUTE_MAX_EXPERTS * 8;
     w.tile_cnt = off; off = align_up(off + (size_t)(L->cols[0] / 16) * sizeof(int), 256);
     w.ublob = off; off = align_up(off + (size_t)w.max_u * sizeof(void*), 256);
     w.uw = off; off = align_up(off + (size_t)w.max_u * 4 * sizeof(float), 256);
@@ -1132,7 +1172,6 @@ static WsLayout ws_layout(const WispExpertLayout* L, int M, int top_k, int has_s
     w.n_q_max = w.max_u * upe;
     w.part = off; off = align_up(off + (size_t)w.n_q_max * M * L->cols[0] * 4, 256);
     w.hcnt = off; off = align_up(off + (size_t)w.max_u * upe * DEC_HCNT_STRIDE * sizeof(int), 256);
-    w.rwords = off; off = align_up(off + (size_t)M * DEC_ROUTE_MAX_EXPERTS * 8, 256);
     const size_t gtiles = (size_t)w.max_u * (L->rows[0] / 16);
     const int gsplit = fused_shape((int)(L->cols[0] / 128)).gsplit;
     w.gcnt = off; off = align_up(off + (gsplit > 1 ? gtiles * sizeof(int) : 0), 256);
@@ -1223,7 +1262,18 @@ static void launch_ng(int ng, bool hz, const DecodeParams& P, hipStream_t s) {
     }
 }
 
-/* Shared body of the two decode entry points: R.mode selects where the
+/* Bounded-wait settings of every launch: the poll limit, and an amount
+ * added to every wait target. Only wisp_amd__test_decode_wait changes them,
+ * to make waits give up on purpose (every kernel still exits normally). */
+static int g_poll_limit = DEC_POLL_LIMIT;
+static int g_poll_extra = 0;
+
+extern "C" void wisp_amd__test_decode_wait(int poll_limit, int extra) {
+    g_poll_limit = poll_limit > 0 ? poll_limit : DEC_POLL_LIMIT;
+    g_poll_extra = extra;
+}
+
+/* Shared body of the decode entry points: R.mode selects where the
  * routing comes from (see RouteArgs). */
 static hipError_t decode_run(const void* const* d_expert_table, const void* d_shared_blob,
                              const WispExpertLayout* L, const void* d_x, int x_dtype, int M,
@@ -1274,6 +1324,9 @@ static hipError_t decode_run(const void* const* d_expert_table, const void* d_sh
     P.out32 = d_out_f32;
     P.out16 = (uint16_t*)d_out_f16;
     P.accumulate = accumulate ? 1 : 0;
+    P.status = (uint32_t*)(ws + DEC_STATUS_OFFSET);
+    P.poll_limit = g_poll_limit;
+    P.poll_extra = g_poll_extra;
 
     const size_t lds = prep_lds_bytes(R.mode, n_experts, M);
     int grid = 1;
@@ -1309,11 +1362,13 @@ static hipError_t decode_run(const void* const* d_expert_table, const void* d_sh
     return hipGetLastError();
 }
 
+/* n_experts is bounded by the prep workgroup's LDS copy of the expert
+ * table (DEC_ROUTE_MAX_EXPERTS entries). */
 static bool decode_args_ok(const void* table, const void* x, int x_dtype, int M, int top_k,
                            int n_experts, const void* ws, const float* o32, const wisp_half* o16) {
     return M >= 1 && M <= DEC_MAX_TOKENS && top_k >= 1 && top_k <= DEC_MAX_TOPK &&
-           n_experts >= 1 && table && x && ws && (o32 || o16) &&
-           (x_dtype == WISP_DTYPE_F16 || x_dtype == WISP_DTYPE_F32);
+           n_experts >= 1 && n_experts <= DEC_ROUTE_MAX_EXPERTS && table && x && ws &&
+           (o32 || o16) && (x_dtype == WISP_DTYPE_F16 || x_dtype == WISP_DTYPE_F32);
 }
 
 extern "C" hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table,
@@ -1339,19 +1394,22 @@ hipError_t wisp_amd__router_logits(const wisp_half* W, const wisp_half* bias, co
                                    int x_dtype, int n_tokens, int hidden, int n_experts,
                                    int add_bias, float* logits, hipStream_t s);
 
-extern "C" hipError_t wisp_gpu_moe_layer_decode_int4(
-    const wisp_half* d_router_w, const wisp_half* d_router_bias, int router_kind,
-    float* d_scores, int* d_topk_idx, float* d_topk_w, const void* const* d_expert_table,
-    const void* d_shared_blob, const WispExpertLayout* L, const void* d_x, int x_dtype,
-    int n_tokens, int top_k, int n_experts, void* d_workspace, size_t workspace_bytes,
-    int accumulate, float* d_out_f32, wisp_half* d_out_f16, hipStream_t s) {
-    if (!decode_args_ok(d_expert_table, d_x, x_dtype, n_tokens, top_k, n_experts, d_workspace,
-                        d_out_f32, d_out_f16) ||
-        !d_router_w || !d_scores || !d_topk_idx || !d_topk_w || top_k > n_experts ||
-        n_experts > DEC_ROUTE_MAX_EXPERTS ||
-        (router_kind != WISP_ROUTER_SOFTMAX && router_kind != WISP_ROUTER_SIGMOID))
-        return hipErrorInvalidValue;
-    if (wisp_expert_layout_check(L) != hipSuccess) return hipErrorInvalidValue;
+static bool layer_args_ok(const wisp_half* d_router_w, int router_kind, const float* d_scores,
+                          const int* d_topk_idx, const float* d_topk_w, int top_k, int n_experts,
+                          const WispExpertLayout* L) {
+    return d_router_w && d_scores && d_topk_idx && d_topk_w && top_k <= n_experts &&
+           (router_kind == WISP_ROUTER_SOFTMAX || router_kind == WISP_ROUTER_SIGMOID) &&
+           wisp_expert_layout_check(L) == hipSuccess;
+}
+
+/* Body of the two layer entry points, arguments already checked. */
+static hipError_t layer_run(const wisp_half* d_router_w, const wisp_half* d_router_bias,
+                            int router_kind, float* d_scores, int* d_topk_idx, float* d_topk_w,
+                            const void* const* d_expert_table, const void* d_shared_blob,
+                            const WispExpertLayout* L, const void* d_x, int x_dtype, int n_tokens,
+                            int top_k, int n_experts, void* d_workspace, size_t workspace_bytes,
+                            int accumulate, float* d_out_f32, wisp_half* d_out_f16,
+                            hipStream_t s) {
     const int hidden = (int)L->cols[0];
     /* the router GEMV runs in router workgroups of the prep launch (mode 3):
      * each thread takes at most 2 16-byte pieces of a row, so rows up to
@@ -1373,4 +1431,40 @@ extern "C" hipError_t wisp_gpu_moe_layer_decode_int4(
     }
     return decode_run(d_expert_table, d_shared_blob, L, d_x, x_dtype, n_tokens, R, top_k,
                       n_experts, d_workspace, workspace_bytes, accumulate, d_out_f32, d_out_f16, s);
+}
+
+extern "C" hipError_t wisp_gpu_moe_layer_decode_int4(
+    const wisp_half* d_router_w, const wisp_half* d_router_bias, int router_kind,
+    float* d_scores, int* d_topk_idx, float* d_topk_w, const void* const* d_expert_table,
+    const void* d_shared_blob, const WispExpertLayout* L, const void* d_x, int x_dtype,
+    int n_tokens, int top_k, int n_experts, void* d_workspace, size_t workspace_bytes,
+    int accumulate, float* d_out_f32, wisp_half* d_out_f16, hipStream_t s) {
+    if (!decode_args_ok(d_expert_table, d_x, x_dtype, n_tokens, top_k, n_experts, d_workspace,
+                        d_out_f32, d_out_f16) ||
+        !layer_args_ok(d_router_w, router_kind, d_scores, d_topk_idx, d_topk_w, top_k, n_experts,
+                       L))
+        return hipErrorInvalidValue;
+    return layer_run(d_router_w, d_router_bias, router_kind, d_scores, d_topk_idx, d_topk_w,
+                     d_expert_table, d_shared_blob, L, d_x, x_dtype, n_tokens, top_k, n_experts,
+                     d_workspace, workspace_bytes, accumulate, d_out_f32, d_out_f16, s);
+}
+
+extern "C" hipError_t wisp_moe_decode_status(void* d_workspace, hipStream_t s, uint32_t* flags,
+                                             int clear) {
+    if (!flags) return hipErrorInvalidValue;
+    *flags = 0;
+    char* ws = (char*)d_workspace;
+    if (!ws) return hipErrorInvalidValue;
+    hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return e;
+    uint32_t v = 0;
+    e = hipMemcpy(&v, ws + DEC_STATUS_OFFSET, sizeof(v), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return e;
+    if (clear && v) {
+        const uint32_t zero = 0;
+        e = hipMemcpy(ws + DEC_STATUS_OFFSET, &zero, sizeof(zero), hipMemcpyHostToDevice);
+        if (e != hipSuccess) return e;
+    }
+    *flags = v;
+    return hipSuccess;
 }

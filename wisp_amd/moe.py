@@ -138,3 +138,17 @@ def expert_offsets(topk_idx: int, n_tokens: int, top_k: int, n_experts: int, cou
     rc = lib().wisp_gpu_expert_offsets(topk_idx, n_tokens, top_k, n_experts, counts, offsets,
                                        order, inv, stream or None)
     _ck(rc, "wisp_gpu_expert_offsets")
+
+
+DECODE_ROUTER_WAIT = 1
+DECODE_DOWN_WAIT = 2
+
+
+def decode_status(ws: DeviceBuffer | None, stream: int = 0, clear: bool = True) -> int:
+    """Sticky status bits of the bounded waits of decode calls on `ws`
+    (waits for `stream`); 0 when every wait completed."""
+    flags = ctypes.c_uint32(0)
+    rc = lib().wisp_moe_decode_status(ws.ptr if ws is not None else None, stream or None,
+                                      ctypes.byref(flags), 1 if clear else 0)
+    _ck(rc, "wisp_moe_decode_status")
+    return int(flags.value)
