@@ -1,20 +1,30 @@
 """Benchmark of the int4 routed-expert MoE layer on one MI355X.
 
-Headline workload: one Mixtral-8x7B-shape MoE layer decode, M = 1 token:
-router GEMV + softmax top-2 on the device, then the fused int4 expert FFN
-(gate/up/SiLU, down, weighted combine) over the 2 routed experts; 8 experts
-of hidden 4096 / inter 14336, int4 g128, fp16 scales, all resident in HBM.
-One step = one MoE layer on one synthetic token (one library call:
-wisp_gpu_moe_layer_decode_int4). `value` is the mean device microseconds per
-layer over K consecutive layers replayed from one HIP graph (how a serving
-loop issues a decode step); the eager, Python-launched figure is reported
-beside it (lower is better for both).
+Headline workload: one DeepSeek-V3-shape MoE layer decode, M = 1 token:
+sigmoid router GEMV + top-8 of 256 routed experts on the device, then the
+fused int4 expert FFN (gate/up/SiLU, down, weighted combine) over the 8
+routed experts and the always-on shared expert; hidden 7168, inter 2048,
+int4 g128, fp16 scales, all resident in HBM. One step = one MoE layer on one
+synthetic token (one library call: wisp_gpu_moe_layer_decode_int4).
 
-Also reported (same JSON line, "extra"): Mixtral M=4 and DeepSeek-V3-shape
-decode (256 routed experts + 1 shared, inter 2048, hidden 7168, sigmoid
-top-8) for M = 1, 2, 4, each with its dominant-kernel roofline.
+Cold weights: the 256 MB Infinity Cache could hold a layer's shared expert
+and router between steps, so steps rotate over 2 full expert sets (2 x 256
+routed experts, 11.6 GB), 16 shared-expert/router variants and a pool of 16
+tokens; the same (set, variant, token) recurs only every 16 layers, after
+about 3 GB of other weights.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+`value` is the median over R >= 5 replays of one HIP graph holding K
+consecutive layers (how a serving loop issues decode steps) of the device
+microseconds per layer; min and max over the replays are reported beside
+it, with the eager (Python-launched) figure. Lower is better.
+
+Also reported ("extra"): DeepSeek-V3 M = 2, 4 and Mixtral-8x7B M = 1, 4
+decode layers, the DeepSeek-V3 2048-token prefill grouped GEMM (MFMA
+fraction of the routed FLOPs, and with the shared expert), and 8-layer
+DeepSeek-V3 expert streaming through the VRAM tier.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--replays R]
+                       [--no-cpu] [--quick]
 """
 from __future__ import annotations
 
@@ -31,6 +41,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E peak
+MFMA_F16_PEAK_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
 EV_ROUTE, EV_PREP, EV_GATEUP, EV_DOWN, EV_COMBINE, EV_PF_GATEUP, EV_PF_DOWN, EV_KINDS = \
     0, 1, 2, 3, 4, 5, 6, 7
 
@@ -40,18 +51,18 @@ def log(msg):
 
 
 class Layer:
-    """Device state of one MoE layer workload.
+    """Device state of one MoE decode-layer workload.
 
-    To measure weights streamed from HBM rather than from the 256 MB
-    Infinity Cache, steps rotate over `n_sets` independent expert sets (each
-    a full layer of resident experts) and a pool of `n_pool` different input
-    tokens (so routing, and with it the touched experts, changes per step).
+    Steps rotate over `n_sets` independent sets of routed experts (each a
+    full layer), `n_var` shared-expert + router variants and a pool of
+    `n_pool` tokens, so that timed steps read weights from HBM rather than
+    from the Infinity Cache.
     """
 
-    def __init__(self, shape, M, seed, n_sets=1, n_pool=16):
+    def __init__(self, shape, M, seed, n_sets=1, n_var=1, n_pool=16):
         from wisp_amd import moe, synth
         from wisp_amd.hip import DeviceBuffer, Stream, to_device
-        self.shape, self.M, self.n_pool = shape, M, n_pool
+        self.shape, self.M, self.n_pool, self.seed = shape, M, n_pool, seed
         rng = np.random.default_rng(seed)
         t0 = time.time()
         keep = range(shape.n_experts) if shape.n_experts <= 8 else ()
@@ -59,20 +70,21 @@ class Layer:
         for si in range(n_sets):
             self.arenas.append(moe.ExpertArena(
                 shape.n_experts, shape.inter, shape.hidden, shape.group_size,
-                lambda e, out, si=si: synth.make_blob(np.random.default_rng([seed, si, e]),
-                                                      shape.inter, shape.hidden, shape.group_size,
-                                                      expert=e, out=out),
+                lambda e, out, si=si: synth.bench_expert(shape, seed, si, e, out),
                 has_zeros=False, keep_host=keep if si == 0 else ()))
-        self.shared_blob = None
-        self.shared_dev = None
+        self.shared_blobs, self.shared_dev = [], []
         if shape.shared:
-            self.shared_blob = synth.make_blob(np.random.default_rng([seed, 99999]), shape.inter,
-                                               shape.hidden, shape.group_size, expert=99999)
-            self.shared_dev = DeviceBuffer(self.shared_blob.nbytes + 16)
-            self.shared_dev.upload(self.shared_blob, offset=8)
-        log(f"{shape.name} M={M}: {n_sets} expert set(s) resident in {time.time() - t0:.1f}s")
-        self.W = synth.make_router(rng, shape.n_experts, shape.hidden)
-        self.dW = to_device(self.W)
+            for v in range(n_var):
+                b = synth.bench_shared(shape, seed, v)
+                d = DeviceBuffer(b.nbytes + 16)
+                d.upload(b, offset=8)
+                self.shared_blobs.append(b if v == 0 else None)
+                self.shared_dev.append(d)
+        self.W = [synth.make_router(rng, shape.n_experts, shape.hidden) for _ in range(n_var)]
+        self.dW = [to_device(w) for w in self.W]
+        self.n_var = n_var
+        log(f"{shape.name} M={M}: {n_sets} expert set(s), {n_var} shared/router variant(s) "
+            f"resident in {time.time() - t0:.1f}s")
         self.kind = moe.ROUTER_SOFTMAX if shape.router == "softmax" else moe.ROUTER_SIGMOID
         self.stream = Stream()
         self.set_tokens(M, rng)
@@ -100,35 +112,34 @@ class Layer:
         from wisp_amd import moe
         s = self.shape
         a = self.arenas[i % len(self.arenas)]
-        moe.moe_layer_decode_int4(self.dW.ptr, 0, self.kind, self.logits.ptr, self.idx.ptr,
+        v = i % self.n_var
+        moe.moe_layer_decode_int4(self.dW[v].ptr, 0, self.kind, self.logits.ptr, self.idx.ptr,
                                   self.w.ptr, a.table.ptr,
-                                  self.shared_dev.ptr + 8 if s.shared else 0, a.layout,
+                                  self.shared_dev[v].ptr + 8 if s.shared else 0, a.layout,
                                   self.xptr(i), self.M, s.top_k, s.n_experts, self.ws,
                                   self.out32.ptr, self.out16.ptr, self.stream.handle)
 
     def fused_experts(self):
-        """True when gate/up and down run in one launch: one token (any
-        hidden size; above 32 hidden blocks each gate/up row tile's K axis
-        is split over several workgroups); otherwise two launches."""
+        """True when gate/up and down run in one launch (one token)."""
         return self.M == 1
 
     def separate_router(self):
-        """True when the router GEMV gets its own launch: only for rows longer
-        than 8192 (otherwise it runs in router workgroups of the prep launch)."""
+        """True when the router GEMV gets its own launch (rows over 8192)."""
         return self.shape.hidden > 8192
 
-    def token_bytes(self):
-        """Per pool token: algorithmic HBM bytes (packed + scales; zeros are
-        +0 and not read) of the expert kernel (gate, up and down of every
-        unique expert), the router and the layer, from the routing the
-        device produces for it."""
+    def token_bytes(self, steps):
+        """Per step: algorithmic HBM bytes (packed + scales; zeros are +0 and
+        not read) of the expert kernel(s) (gate, up and down of every unique
+        expert), the router and the layer, from the routing the device
+        produces for that step."""
         from wisp_amd.hip import synchronize
         if self._bytes is None:
             s = self.shape
             mat = (s.inter * s.hidden) // 2 + 2 * (s.inter * s.hidden // s.group_size)
             router = s.n_experts * s.hidden * 2
+            period = int(np.lcm.reduce([self.n_pool, len(self.arenas), self.n_var]))
             out = []
-            for t in range(self.n_pool):
+            for t in range(period):
                 self.step(t)
                 synchronize()
                 ids = self.idx.download(np.int32, (self.M, s.top_k))
@@ -136,19 +147,18 @@ class Layer:
                 out.append({"n_unique": n_u, "experts": 3 * n_u * mat,
                             "router": router, "layer": 3 * n_u * mat + router})
             self._bytes = out
-        return self._bytes
+        return [self._bytes[i % len(self._bytes)] for i in range(steps)]
 
     def mean_bytes(self, steps):
-        tb = self.token_bytes()
-        keys = tb[0].keys()
-        return {k: float(np.mean([tb[i % self.n_pool][k] for i in range(steps)])) for k in keys}
+        tb = self.token_bytes(steps)
+        return {k: float(np.mean([b[k] for b in tb])) for k in tb[0]}
 
 
-def time_layer(layer, steps, warmup):
-    """Device time per layer over `steps` consecutive layers, two ways:
-    replayed from one HIP graph holding all of them (no host launch cost:
-    how a serving loop runs a decode step) and launched eagerly from
-    Python; then the per-kernel durations from events around each kernel."""
+def time_layer(layer, steps, warmup, replays):
+    """Device time per layer over `steps` consecutive layers: replayed from
+    one HIP graph holding all of them `replays` times (median, min, max),
+    launched eagerly from Python once; then the per-kernel durations from
+    events recorded around each kernel on the launch stream."""
     from wisp_amd import _lib
     from wisp_amd.hip import Event, Graph, synchronize
     for i in range(warmup):
@@ -166,13 +176,14 @@ def time_layer(layer, steps, warmup):
     graph = Graph(layer.stream, lambda: [layer.step(i) for i in range(steps)])
     graph.launch(layer.stream)       # warm replay
     synchronize()
-    e0.record(layer.stream.handle)
-    graph.launch(layer.stream)
-    e1.record(layer.stream.handle)
-    synchronize()
-    dev_ms = e0.elapsed_ms(e1)
+    per = []
+    for _ in range(replays):
+        e0.record(layer.stream.handle)
+        graph.launch(layer.stream)
+        e1.record(layer.stream.handle)
+        synchronize()
+        per.append(1e3 * e0.elapsed_ms(e1) / steps)
     del graph
-    # per-kernel durations: same steps again with events around each kernel
     evs = [[Event() for _ in range(2 * EV_KINDS)] for _ in range(steps)]
     arrs = [(ctypes.c_void_p * (2 * EV_KINDS))(*[e.handle for e in row]) for row in evs]
     lib = _lib.lib()
@@ -181,6 +192,7 @@ def time_layer(layer, steps, warmup):
         layer.step(i)
     lib.wisp_amd_set_kernel_events(None, 0)
     synchronize()
+
     def kernel_us(k):
         return 1e3 * float(np.mean([evs[i][2 * k].elapsed_ms(evs[i][2 * k + 1])
                                     for i in range(steps)]))
@@ -195,52 +207,10 @@ def time_layer(layer, steps, warmup):
         kern["gate_up"] = kernel_us(EV_GATEUP)
         kern["down"] = kernel_us(EV_DOWN)
         kern["experts"] = kern["gate_up"] + kern["down"]
-    return {"us_per_layer": 1e3 * dev_ms / steps, "eager_us_per_layer": 1e3 * eager_ms / steps,
+    return {"us_per_layer": float(np.median(per)), "us_min": float(np.min(per)),
+            "us_max": float(np.max(per)), "replays": replays,
+            "eager_us_per_layer": 1e3 * eager_ms / steps,
             "host_us_per_layer": 1e3 * host_ms / steps, "kernel_us": kern}
-
-
-def cpu_baseline(layer, budget_s=10.0):
-    """The oracle's vectorised CPU path (AVX-512 or AVX2, OpenMP over rows)
-    on this host: router + top-k + the routed experts' FFN, one token per
-    layer, cycling over the same token pool as the GPU steps."""
-    from oracle import oracle as O
-    s = layer.shape
-    blobs = layer.arenas[0].host
-
-    def one(i):
-        x = layer.x[i % layer.n_pool, 0].astype(np.float32)
-        idx, w, _ = O.router_topk(layer.W.view(np.uint16), None, x, s.top_k, kind=s.router)
-        acc = np.zeros(s.hidden, np.float32)
-        if layer.shared_blob is not None:
-            O.expert_ffn(layer.shared_blob, x, acc, 1.0, fast=True)
-        for e, we in zip(idx, w):
-            O.expert_ffn(blobs[int(e)], x, acc, float(we), fast=True)
-        return acc
-
-    one(0)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while (time.perf_counter() < t_end and len(times) < 2000) or len(times) < 3:
-        t0 = time.perf_counter()
-        one(len(times))
-        times.append(time.perf_counter() - t0)
-    isa = {2: "avx512", 1: "avx2", 0: "scalar"}[O.orc().orc_fast_isa()]
-    return {"value": round(1e6 * float(np.median(times)), 1), "unit": "us/layer",
-            "cores": int(O.orc().orc_num_threads()), "kind": "port",
-            "sample": f"{len(times)} {s.name} M=1 layers (router + top-{s.top_k} experts), median; "
-                      f"{isa} OpenMP fp32 path of oracle/wisp_oracle.c",
-            "cpu": _cpu_model()}
-
-
-def _cpu_model():
-    try:
-        with open("/proc/cpuinfo") as f:
-            for ln in f:
-                if ln.startswith("model name"):
-                    return ln.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
 
 
 def roofline(nbytes, us):
@@ -258,15 +228,18 @@ def load_traffic(workload):
         return None
 
 
-def measure(layer, steps, warmup):
-    r = time_layer(layer, steps, warmup)
+def measure(layer, steps, warmup, replays):
+    r = time_layer(layer, steps, warmup, replays)
     b = layer.mean_bytes(steps)
     us = r["us_per_layer"]
     return {
         "us_per_layer": round(us, 3),
+        "us_min": round(r["us_min"], 3), "us_max": round(r["us_max"], 3),
+        "replays": r["replays"], "layers_per_replay": steps,
         "eager_us_per_layer": round(r["eager_us_per_layer"], 3),
         "host_us_per_layer": round(r["host_us_per_layer"], 3),
         "layer_hbm_frac": round(b["layer"] / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "layer_bytes": int(b["layer"]),
         "n_unique_experts": round(b["n_unique"], 2),
         "kernel_us": {k: round(v, 3) for k, v in r["kernel_us"].items()},
         "experts": {**roofline(b["experts"], r["kernel_us"]["experts"]),
@@ -274,21 +247,125 @@ def measure(layer, steps, warmup):
     }
 
 
-MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+# ---------------------------------------------------------------------------
+# CPU baseline (the oracle's C restatement, timed on this host's cores)
+# ---------------------------------------------------------------------------
+
+def _cpu_info():
+    model, phys = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            pid = core = None
+            for ln in f:
+                if ln.startswith("model name") and model == "unknown":
+                    model = ln.split(":", 1)[1].strip()
+                elif ln.startswith("physical id"):
+                    pid = ln.split(":", 1)[1].strip()
+                elif ln.startswith("core id"):
+                    core = ln.split(":", 1)[1].strip()
+                    phys.add((pid, core))
+    except OSError:
+        pass
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = os.cpu_count()
+    return {"cpu": model, "logical_cpus_visible": os.cpu_count(), "cpus_in_affinity": aff,
+            "physical_cores_visible": len(phys) or None,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
 
 
-def measure_prefill(layer, n_tokens, steps, warmup, seed=2048):
+def _time_bounded(fn, budget_s, max_runs, min_runs=3):
+    fn(0)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while (time.perf_counter() < t_end and len(times) < max_runs) or len(times) < min_runs:
+        t0 = time.perf_counter()
+        fn(len(times))
+        times.append(time.perf_counter() - t0)
+    return times
+
+
+def cpu_baseline(layer, budget_s=10.0):
+    """The oracle's vectorised CPU path (AVX-512 or AVX2, OpenMP over rows)
+    on this host for the headline workload: router + top-k + the shared and
+    routed experts' FFN, one token per layer, over the same token pool and
+    the first expert set and variant of the GPU steps."""
+    from oracle import oracle as O
+    s = layer.shape
+    blobs = layer.arenas[0].host if layer.arenas[0].host else None
+    if blobs is None:
+        from wisp_amd import synth
+        cache = {}
+
+        def blob(e):
+            if e not in cache:
+                cache[e] = synth.bench_expert(s, layer.seed, 0, e)
+            return cache[e]
+    else:
+        def blob(e):
+            return blobs[e]
+    shared = layer.shared_blobs[0] if layer.shared_blobs else None
+
+    def one(i):
+        x = layer.x[i % layer.n_pool, 0].astype(np.float32)
+        idx, w, _ = O.router_topk(layer.W[0].view(np.uint16), None, x, s.top_k, kind=s.router)
+        acc = np.zeros(s.hidden, np.float32)
+        if shared is not None:
+            O.expert_ffn(shared, x, acc, 1.0, fast=True)
+        for e, we in zip(idx, w):
+            O.expert_ffn(blob(int(e)), x, acc, float(we), fast=True)
+        return acc
+
+    for i in range(layer.n_pool):      # make every routed blob of the pool once
+        one(i)
+    times = _time_bounded(one, budget_s, 5000)
+    isa = {2: "avx512", 1: "avx2", 0: "scalar"}[O.orc().orc_fast_isa()]
+    return {"value": round(1e6 * float(np.median(times)), 1), "unit": "us/layer",
+            "cores": int(O.orc().orc_num_threads()), "kind": "port",
+            "sample": f"{len(times)} {s.name} M=1 layers (router + top-{s.top_k} experts"
+                      f"{' + shared' if shared is not None else ''}), median; {isa} OpenMP fp32 "
+                      f"path of oracle/wisp_oracle.c, about {budget_s:.0f} s of CPU work",
+            **_cpu_info()}
+
+
+def cpu_single_expert(budget_s=8.0):
+    """C1: one Mixtral-8x7B-shape expert FFN (x fp16 [1, 4096]) on the CPU:
+    the vectorised path and the reference-cost scalar restatement (per-element
+    fp16 -> fp32 conversions, as the reference's scalar branch), both OpenMP
+    over rows on every thread."""
+    from oracle import oracle as O
+    from wisp_amd import synth
+    s = synth.MIXTRAL
+    blob = synth.bench_expert(s, synth.MIXTRAL_BENCH_SEED, 0, 0)
+    x = synth.make_x(np.random.default_rng(5), 1, s.hidden)[0].astype(np.float32)
+    nbytes = synth.expert_bytes_no_zeros(s.inter, s.hidden, s.group_size)
+    out = {}
+    for name, fast, budget, runs in (("vectorised", True, budget_s, 2000),
+                                     ("scalar_reference_cost", False, budget_s, 10)):
+        t = _time_bounded(lambda i: O.expert_ffn(blob, x, None, 1.0, fast=fast), budget, runs)
+        us = 1e6 * float(np.median(t))
+        out[name] = {"us": round(us, 1), "gbs": round(nbytes / (us * 1e-6) / 1e9, 2),
+                     "runs": len(t)}
+    isa = {2: "avx512", 1: "avx2", 0: "scalar"}[O.orc().orc_fast_isa()]
+    return {"workload": "one mixtral-8x7b expert FFN, int4 g128, 90,832,896 B of weights",
+            "threads": int(O.orc().orc_num_threads()), "vectorised_isa": isa, **out}
+
+
+# ---------------------------------------------------------------------------
+# prefill and streaming
+# ---------------------------------------------------------------------------
+
+def measure_prefill(layer, n_tokens, steps, warmup, replays):
     """DeepSeek-V3-shape prefill grouped GEMM: n_tokens fp16 tokens, top-8
     drawn without replacement from Zipf(1.1) over the 256 routed experts,
-    plus the shared expert; timed by HIP events on the launch stream
-    (graph replay of `steps` calls, and per-kernel events)."""
+    plus the shared expert (synth.prefill_draw, the draw the config-scale
+    parity test checks); timed by HIP events on the launch stream (graph
+    replays of `steps` calls, and per-kernel events)."""
     from wisp_amd import _lib, moe, synth
     from wisp_amd.hip import DeviceBuffer, Event, Graph, synchronize, to_device
     s = layer.shape
-    rng = np.random.default_rng(seed)
-    idx = synth.zipf_topk(rng, n_tokens, s.n_experts, s.top_k)
-    w = synth.route_weights(rng, n_tokens, s.top_k)
-    x = synth.make_x(rng, n_tokens, s.hidden)
+    idx, w, x = synth.prefill_draw(s, n_tokens)
     dx, di, dw = to_device(x), to_device(idx), to_device(w)
     a = layer.arenas[0]
     ws = DeviceBuffer(moe.prefill_workspace_bytes(a.layout, n_tokens, s.top_k, s.n_experts, s.shared))
@@ -296,8 +373,8 @@ def measure_prefill(layer, n_tokens, steps, warmup, seed=2048):
     st = layer.stream
 
     def step():
-        moe.moe_prefill_int4(a.table.ptr, layer.shared_dev.ptr + 8 if s.shared else 0, a.layout,
-                             dx.ptr, n_tokens, di.ptr, dw.ptr, s.top_k, s.n_experts, ws,
+        moe.moe_prefill_int4(a.table.ptr, layer.shared_dev[0].ptr + 8 if s.shared else 0,
+                             a.layout, dx.ptr, n_tokens, di.ptr, dw.ptr, s.top_k, s.n_experts, ws,
                              out16=out16.ptr, stream=st.handle)
 
     for _ in range(warmup):
@@ -307,12 +384,15 @@ def measure_prefill(layer, n_tokens, steps, warmup, seed=2048):
     graph.launch(st)
     synchronize()
     e0, e1 = Event(), Event()
-    e0.record(st.handle)
-    graph.launch(st)
-    e1.record(st.handle)
-    synchronize()
-    ms = e0.elapsed_ms(e1) / steps
+    per = []
+    for _ in range(replays):
+        e0.record(st.handle)
+        graph.launch(st)
+        e1.record(st.handle)
+        synchronize()
+        per.append(e0.elapsed_ms(e1) / steps)
     del graph
+    ms = float(np.median(per))
     evs = [Event() for _ in range(2 * EV_KINDS)]
     arr = (ctypes.c_void_p * (2 * EV_KINDS))(*[e.handle for e in evs])
     lib = _lib.lib()
@@ -324,19 +404,26 @@ def measure_prefill(layer, n_tokens, steps, warmup, seed=2048):
     dn_ms = evs[2 * EV_PF_DOWN].elapsed_ms(evs[2 * EV_PF_DOWN + 1])
     counts = np.bincount(idx.reshape(-1), minlength=s.n_experts)
     pairs_routed = int(counts.sum())
+    pairs_all = pairs_routed + (n_tokens if s.shared else 0)
     per_pair = 3 * 2 * s.hidden * s.inter
-    flops = per_pair * (pairs_routed + (n_tokens if s.shared else 0))
-    tflops = flops / (ms * 1e-3) / 1e12
-    gu_flops = 2 * 2 * s.hidden * s.inter * (pairs_routed + (n_tokens if s.shared else 0))
-    dn_flops = 2 * s.hidden * s.inter * (pairs_routed + (n_tokens if s.shared else 0))
+    flops_routed = per_pair * pairs_routed
+    flops_all = per_pair * pairs_all
+    tf_routed = flops_routed / (ms * 1e-3) / 1e12
+    tf_all = flops_all / (ms * 1e-3) / 1e12
+    gu_flops = 2 * 2 * s.hidden * s.inter * pairs_all
+    dn_flops = 2 * s.hidden * s.inter * pairs_all
     used = int((counts > 0).sum()) + (1 if s.shared else 0)
     wbytes = used * synth.expert_bytes_no_zeros(s.inter, s.hidden, s.group_size)
     return {
-        "ms_per_layer": round(ms, 4), "tokens": n_tokens,
+        "ms_per_layer": round(ms, 4), "ms_min": round(float(np.min(per)), 4),
+        "ms_max": round(float(np.max(per)), 4), "replays": replays, "tokens": n_tokens,
         "tokens_per_s": round(n_tokens / (ms * 1e-3), 1),
-        "flops": flops, "tflops": round(tflops, 2),
-        "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
-        "weight_bytes_unique": wbytes, "weight_hbm_frac": round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "flops_routed": flops_routed, "tflops_routed": round(tf_routed, 2),
+        "mfma_frac_routed": round(tf_routed / MFMA_F16_PEAK_TFLOPS, 4),
+        "flops_with_shared": flops_all, "tflops_with_shared": round(tf_all, 2),
+        "mfma_frac_with_shared": round(tf_all / MFMA_F16_PEAK_TFLOPS, 4),
+        "weight_bytes_unique": wbytes,
+        "weight_hbm_frac": round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "group_sizes": {"max": int(counts.max()), "median": float(np.median(counts)),
                         "empty": int((counts == 0).sum())},
         "kernel_ms": {"gate_up": round(gu_ms, 4), "down": round(dn_ms, 4)},
@@ -349,19 +436,18 @@ def measure_streaming(n_layers=8, steps=256, slot_frac=0.30, seed=55, n_template
     """Expert-streaming decode: n_layers DeepSeek-V3-shape MoE layers whose
     256 routed experts each live in pinned host RAM, a VRAM LRU of slot_frac
     of all experts (the tier of include/wisp_amd.h section 6), one token per
-    step with Zipf(1.1) top-8 routing per layer, the shared expert resident.
-    The compute stream is synchronised after every layer, as a real decode
-    must (the next layer's routing needs this layer's output). Reports
-    us/token over all steps and over the second half (warm), the VRAM hit
-    rate (vram_hits / lookups) and the H2D rate, plus the rate of a plain
-    run of blob copies for comparison."""
+    step with Zipf(1.1) top-8 routing per layer (synth.streaming_draw), the
+    shared expert resident. The compute stream is synchronised after every
+    layer, as a real decode must (the next layer's routing needs this
+    layer's output). Reports us/token over all steps and over the second
+    half (warm), the VRAM hit rate (vram_hits / lookups) and the H2D rate,
+    plus the rate of a plain run of blob copies for comparison."""
     from wisp_amd import moe, synth, tier
     from wisp_amd.hip import DeviceBuffer, Event, PinnedBuffer, Stream, synchronize, to_device
     s = synth.DSV3
     E, k = s.n_experts, s.top_k
     size = synth.blob_size(s.inter, s.hidden, s.group_size)
     t0 = time.time()
-    rng = np.random.default_rng(seed)
     temps = [synth.make_blob(np.random.default_rng([seed, i]), s.inter, s.hidden, s.group_size,
                              expert=i) for i in range(n_templates)]
     layers = []
@@ -384,9 +470,8 @@ def measure_streaming(n_layers=8, steps=256, slot_frac=0.30, seed=55, n_template
     st = Stream()
     ws = DeviceBuffer(moe.decode_workspace_bytes(layout, 1, k, True))
     out32 = DeviceBuffer(4 * s.hidden)
-    xs = to_device(synth.make_x(rng, 16, s.hidden))
-    routes = [[synth.zipf_topk(rng, 1, E, k) for _ in range(n_layers)] for _ in range(steps)]
-    weights = [[synth.route_weights(rng, 1, k) for _ in range(n_layers)] for _ in range(steps)]
+    xs_h, routes, weights = synth.streaming_draw(s, n_layers, steps, seed=seed)
+    xs = to_device(xs_h)
     per_step = []
     half = None
     for step in range(steps):
@@ -451,11 +536,17 @@ def copy_calibration(mib):
     print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
 
 
+def dsv3_layer(M):
+    from wisp_amd import synth
+    return Layer(synth.DSV3, M, seed=synth.DSV3_BENCH_SEED, n_sets=2, n_var=16)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=32)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--replays", type=int, default=7)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline workload only")
     ap.add_argument("--prefill-only", action="store_true",
@@ -465,6 +556,8 @@ def main():
     ap.add_argument("--stream-steps", type=int, default=256)
     ap.add_argument("--dsv3-decode-only", type=int, default=0, metavar="M",
                     help="only the DeepSeek-V3 decode layer with M tokens (profiling runs)")
+    ap.add_argument("--mixtral-decode-only", type=int, default=0, metavar="M",
+                    help="only the Mixtral-8x7B decode layer with M tokens (profiling runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB 5 times (byte-counter calibration)")
     args = ap.parse_args()
@@ -472,6 +565,7 @@ def main():
         print("bench.py measures one GPU only: the int4 MoE expert path here is a single-GPU "
               "build; expert-parallel sharding over several GPUs is not run", file=sys.stderr)
         sys.exit(2)
+    steps, warmup, replays = max(1, args.steps), max(0, args.warmup), max(5, args.replays)
 
     from wisp_amd import synth
     from wisp_amd.hip import device_count
@@ -483,46 +577,53 @@ def main():
         return
 
     if args.dsv3_decode_only:
-        ds = Layer(synth.DSV3, args.dsv3_decode_only, seed=777, n_sets=1)
-        r = measure(ds, args.steps, args.warmup)
+        ds = dsv3_layer(args.dsv3_decode_only)
+        r = measure(ds, steps, warmup, replays)
         print(json.dumps({f"deepseek-v3-decode-m{args.dsv3_decode_only}": r}), flush=True)
         return
-
+    if args.mixtral_decode_only:
+        mx = Layer(synth.MIXTRAL, args.mixtral_decode_only, seed=synth.MIXTRAL_BENCH_SEED, n_sets=4)
+        r = measure(mx, steps, warmup, replays)
+        print(json.dumps({f"mixtral-8x7b-decode-m{args.mixtral_decode_only}": r}), flush=True)
+        return
     if args.streaming_only:
         r = measure_streaming(steps=args.stream_steps)
         print(json.dumps({"deepseek-v3-streaming-8layers": r}), flush=True)
         return
-
     if args.prefill_only:
-        ds = Layer(synth.DSV3, 1, seed=777, n_sets=1)
-        r = measure_prefill(ds, 2048, max(2, min(args.steps, 10)), 2)
+        ds = dsv3_layer(1)
+        r = measure_prefill(ds, 2048, max(2, min(steps, 10)), 2, replays)
         print(json.dumps({"deepseek-v3-prefill-2048": r}), flush=True)
         return
 
-    # 4 Mixtral expert sets (3 GB) so consecutive steps stream cold weights
-    head = Layer(synth.MIXTRAL, 1, seed=1234, n_sets=4)
-    m = measure(head, args.steps, args.warmup)
-    log(f"mixtral M=1: {m['us_per_layer']:.2f} us/layer, kernels {m['kernel_us']}")
+    head = dsv3_layer(1)
+    m = measure(head, steps, warmup, replays)
+    log(f"deepseek-v3 M=1: {m['us_per_layer']:.2f} us/layer (min {m['us_min']:.2f}, "
+        f"max {m['us_max']:.2f}), kernels {m['kernel_us']}")
     gu = dict(m["experts"])
-    gu["traffic"] = load_traffic("mixtral-decode-m1/experts")
+    gu["traffic"] = load_traffic("deepseek-v3-decode-m1/experts")
     result = {
-        "metric": "us per MoE layer, int4 expert decode (Mixtral-8x7B shape, M=1)",
+        "metric": "us per MoE layer, int4 expert decode (DeepSeek-V3 shape, M=1)",
         "value": m["us_per_layer"],
         "unit": "us/layer",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(m["us_per_layer"] / 1e3, 6),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16",
-        "data": "synthetic",
-        "config": {"workload": "mixtral-8x7b-moe-decode-m1", "hidden": 4096, "inter": 14336,
-                   "experts": 8, "top_k": 2, "tokens": 1, "weights": "int4 g128 fp16 scales",
-                   "router": "softmax top-2 on device", "expert_sets_rotated": 4,
-                   "parallelism": "single-gpu"},
+        "dtype": "int4 weights, fp16 activations, fp32 accumulate",
+        "data": "synthetic (seeded int4 weights and fp16 tokens of the named shape)",
+        "config": {"workload": "deepseek-v3-moe-decode-m1", "hidden": 7168, "inter": 2048,
+                   "routed_experts": 256, "shared_experts": 1, "top_k": 8, "tokens": 1,
+                   "weights": "int4 g128 fp16 scales",
+                   "router": "sigmoid top-8 on device (uniform-like random choice)",
+                   "expert_sets_rotated": 2, "shared_router_variants_rotated": 16,
+                   "token_pool": 16, "parallelism": "single-gpu"},
+        "us_min": m["us_min"], "us_max": m["us_max"], "replays": m["replays"],
         "layer_hbm_frac": m["layer_hbm_frac"],
+        "layer_bytes": m["layer_bytes"],
         "kernel_us": m["kernel_us"],
         "roofline": {"bound": gu["bound"], "achieved": gu["achieved"], "peak": gu["peak"],
                      "unit": gu["unit"], "frac": gu["frac"], "traffic": gu["traffic"],
@@ -537,22 +638,28 @@ def main():
     if not args.quick:
         extra = {}
         rng = np.random.default_rng(99)
-        head.set_tokens(4, rng)
-        extra["mixtral-8x7b-decode-m4"] = measure(head, max(20, args.steps // 2), 5)
-        log(f"mixtral M=4: {extra['mixtral-8x7b-decode-m4']}")
-        del head
-        ds = Layer(synth.DSV3, 1, seed=777, n_sets=1)
-        for M in (1, 2, 4):
-            if M > 1:
-                ds.set_tokens(M, rng)
+        sub = max(16, steps // 2)
+        for M in (2, 4):
+            head.set_tokens(M, rng)
             key = f"deepseek-v3-decode-m{M}"
-            extra[key] = measure(ds, max(20, args.steps // 2), 5)
-            log(f"{key}: {extra[key]}")
-        extra["deepseek-v3-prefill-2048"] = measure_prefill(ds, 2048, 5, 2)
+            extra[key] = measure(head, sub, 4, replays)
+            log(f"{key}: {extra[key]['us_per_layer']} us, kernels {extra[key]['kernel_us']}")
+        extra["deepseek-v3-prefill-2048"] = measure_prefill(head, 2048, 5, 2, replays)
         log(f"deepseek-v3 prefill: {extra['deepseek-v3-prefill-2048']}")
-        del ds
+        del head
+        mx = Layer(synth.MIXTRAL, 1, seed=synth.MIXTRAL_BENCH_SEED, n_sets=4)
+        for M in (1, 4):
+            if M > 1:
+                mx.set_tokens(M, rng)
+            key = f"mixtral-8x7b-decode-m{M}"
+            extra[key] = measure(mx, sub, 4, replays)
+            log(f"{key}: {extra[key]['us_per_layer']} us, kernels {extra[key]['kernel_us']}")
+        del mx
         extra["deepseek-v3-streaming-8layers"] = measure_streaming(steps=args.stream_steps)
         log(f"streaming: {extra['deepseek-v3-streaming-8layers']}")
+        if not args.no_cpu:
+            extra["cpu_c1_single_mixtral_expert"] = cpu_single_expert()
+            log(f"cpu C1: {extra['cpu_c1_single_mixtral_expert']}")
         result["extra"] = extra
     print(json.dumps(result), flush=True)
 

@@ -221,9 +221,11 @@ enum {
     WISP_DECODE_DOWN_WAIT = 2      /* a down projection never saw its h'    */
 };
 
-/* Waits for stream s, then returns in *flags the sticky status bits that
- * decode calls on d_workspace have set since it was last cleared (0: every
- * wait completed), and clears them when clear != 0. Synchronous. */
+/* Waits for stream s, then returns in *flags the status bits of the most
+ * recent decode call on d_workspace (0: every wait of that call completed;
+ * each call starts from 0, so check after every call that matters), and
+ * clears them when clear != 0. Undefined before the first call.
+ * Synchronous. */
 hipError_t wisp_moe_decode_status(void* d_workspace, hipStream_t s,
                                   uint32_t* flags, int clear);
 

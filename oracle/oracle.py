@@ -68,6 +68,19 @@ def orc():
     return _ORC
 
 
+def ref_built() -> bool:
+    """Whether oracle/_ref was built here (checks the file; loads nothing)."""
+    return (HERE / "_ref" / "libwisp_ref.so").exists()
+
+
+class LazyRef:
+    """Attribute access loads the reference build on first use, so importing
+    a test module maps nothing into the process."""
+
+    def __getattr__(self, name):
+        return getattr(ref(), name)
+
+
 def ref():
     """The compiled reference CPU path, or None when it was not built here."""
     global _REF
@@ -146,8 +159,20 @@ def expert_ffn(blob: np.ndarray, x: np.ndarray, acc: np.ndarray | None = None, w
     return acc
 
 
-def moe_combine(blobs: list, shared_blob, x, idx, w) -> np.ndarray:
-    """One token: shared (w = 1) then routed experts in rank order."""
+def moe_combine(blobs: list, shared_blob, x, idx, w, fast: bool = False) -> np.ndarray:
+    """One token: shared (w = 1) then routed experts in rank order. With
+    fast=True each expert runs on the vectorised path (orc_expert_ffn_fast,
+    itself checked against the scalar one), in the same order."""
+    if fast:
+        x32 = np.ascontiguousarray(x, dtype=np.float32)
+        m = parse_blob(blobs[0] if blobs else shared_blob)
+        out = np.zeros(int(m.rows[2]), np.float32)
+        if shared_blob is not None:
+            expert_ffn(shared_blob, x32, out, 1.0, fast=True)
+        for e, we in zip(np.asarray(idx).reshape(-1), np.asarray(w).reshape(-1)):
+            if e >= 0:
+                expert_ffn(blobs[int(e)], x32, out, float(we), fast=True)
+        return out
     m = parse_blob(blobs[0] if blobs else shared_blob)
     hidden, inter = int(m.rows[2]), int(m.rows[0])
     arr = (c_void_p * max(1, len(blobs)))(*[b.ctypes.data for b in blobs])

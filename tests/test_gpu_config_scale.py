@@ -1,0 +1,164 @@
+"""GPU parity at the full sizes of the two benchmarked workloads that are
+not single decode layers.
+
+* DeepSeek-V3 prefill, 2048 tokens: the benchmark's own draw (top-8 of 256
+  experts from Zipf(1.1), seed 2048) over the benchmark's expert set, so
+  the wide full-tile kernels see full 128-token tiles, experts split over
+  many tiles (the largest group is 1,805 tokens) and every smaller class.
+  Checked tokens are chosen from the routing: the first, boundary and last
+  tokens of the largest expert's tiles, tokens with a pair in a remainder
+  tile of each smaller class (<= 32, <= 64, < 128 tokens), the token of the
+  rarest expert, the first and last tokens and a spread over the batch.
+* Expert streaming: 8 DeepSeek-V3 layers x 256 experts in pinned host RAM
+  (48 GB), a VRAM tier of 614 slots (30 %) and a scratch ring of top-k + 2,
+  96 decode steps of Zipf(1.1) top-8 routing; every layer of every step is
+  checked against the oracle, the copy accounting is exact, and the run
+  reaches promotions and evictions.
+
+Oracle: moe_combine with the vectorised expert FFN (pinned against the
+scalar restatement in tests/test_oracle.py). Bar: tests/gpu_util.py.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.gpu_util import assert_close
+from wisp_amd import moe, synth, tier
+from wisp_amd.hip import DeviceBuffer, PinnedBuffer, Stream, synchronize, to_device
+
+pytestmark = pytest.mark.gpu
+
+DS = synth.DSV3
+
+
+def _pick_prefill_tokens(idx):
+    """Token ids that exercise every tile class and the multi-tile expert."""
+    E = DS.n_experts
+    counts = np.bincount(idx.reshape(-1), minlength=E)
+    big = int(np.argmax(counts))
+    toks_big = [t for t in range(idx.shape[0]) if big in idx[t]]   # flat order = tile order
+    pick = {0, idx.shape[0] - 1}
+    pick.update(toks_big[:2])                                 # first tile
+    for b in (127, 128, 255, 256):                            # tile boundaries
+        if b < len(toks_big):
+            pick.add(toks_big[b])
+    pick.update(toks_big[-2:])                                # the tail tile
+    # tokens with a pair in a tile of each smaller class: remainders of
+    # <= 32, 33..64 and 65..127 tokens
+    rem = counts % 128
+    for lo, hi in ((1, 32), (33, 64), (65, 127)):
+        hit = [t for t in range(idx.shape[0]) if ((rem[idx[t]] >= lo) & (rem[idx[t]] <= hi)).any()]
+        pick.update(hit[:3])
+        pick.update(hit[-1:])
+    # the token routed to the rarest used expert
+    used = np.nonzero(counts)[0]
+    rare = used[np.argmin(counts[used])]
+    pick.add(int(next(t for t in range(idx.shape[0]) if rare in idx[t])))
+    pick.update(range(200, idx.shape[0], 256))                # spread over the batch
+    return sorted(pick), big, counts
+
+
+def test_dsv3_prefill_2048_benchmark_draw():
+    print("config scale: DeepSeek-V3 prefill, 2048 tokens, benchmark draw", flush=True)
+    T = 2048
+    idx, w, x = synth.prefill_draw(DS, T, seed=synth.PREFILL_SEED)
+    tokens, big, counts = _pick_prefill_tokens(idx)
+    assert counts[big] > 2 * 128 and len(tokens) >= 16, (counts[big], len(tokens))
+    seed = synth.DSV3_BENCH_SEED
+    arena = moe.ExpertArena(DS.n_experts, DS.inter, DS.hidden, DS.group_size,
+                            lambda e, out: synth.bench_expert(DS, seed, 0, e, out),
+                            has_zeros=False)
+    sh_blob = synth.bench_shared(DS, seed, 0)
+    sh = DeviceBuffer(sh_blob.nbytes + 16)
+    sh.upload(sh_blob, offset=8)
+    dx, di, dw = to_device(x), to_device(idx), to_device(w)
+    ws = DeviceBuffer(moe.prefill_workspace_bytes(arena.layout, T, DS.top_k, DS.n_experts, True))
+    out32, out16 = DeviceBuffer(4 * T * DS.hidden), DeviceBuffer(2 * T * DS.hidden)
+    print(f"  experts resident; checking {len(tokens)} tokens (largest group {counts[big]} "
+          f"tokens on expert {big})", flush=True)
+    moe.moe_prefill_int4(arena.table.ptr, sh.ptr + 8, arena.layout, dx.ptr, T, di.ptr, dw.ptr,
+                         DS.top_k, DS.n_experts, ws, out32.ptr, out16.ptr)
+    synchronize()
+    g32 = out32.download(np.float32, (T, DS.hidden))
+    g16 = out16.download(np.float16, (T, DS.hidden)).astype(np.float32)
+    need = sorted({int(e) for t in tokens for e in idx[t]})
+    cache = {e: synth.bench_expert(DS, seed, 0, e) for e in need}
+    blobs = [cache.get(e, cache[need[0]]) for e in range(DS.n_experts)]
+    for t in tokens:
+        want = O.moe_combine(blobs, sh_blob, x[t].astype(np.float32), idx[t], w[t], fast=True)
+        assert_close(g32[t], want, f"token {t} fp32 (experts {idx[t].tolist()})")
+        assert_close(g16[t], want, f"token {t} fp16")
+    assert np.isfinite(g32).all()
+
+
+def _fill_streaming_blobs(pinned, L, E, size):
+    """Every (layer, expert) blob distinct: header and scale sections from one
+    of 16 seeded templates, packed nibbles from a per-blob byte stream."""
+    temps = [synth.make_blob(np.random.default_rng([55, i]), DS.inter, DS.hidden,
+                             DS.group_size, expert=i) for i in range(16)]
+    secs = synth.section_offsets(DS.inter, DS.hidden, DS.group_size)
+    for l in range(L):
+        for e in range(E):
+            off = (l * E + e) * size
+            blob = pinned.array[off:off + size]
+            blob[:] = temps[(l * E + e) % 16]
+            for m, (p, s_, z, r, c) in enumerate(secs):
+                O.orc().orc_fill_random_bytes(blob[p:s_].ctypes.data, s_ - p,
+                                              (l * E + e) * 3 + m + 1)
+        print(f"  layer {l}: {E} blobs written", flush=True)
+
+
+def test_streaming_tier_dsv3_8_layers_614_slots():
+    print("config scale: 8-layer DeepSeek-V3 streaming, 614 VRAM slots", flush=True)
+    L, E, k, steps = 8, DS.n_experts, DS.top_k, 96
+    size = synth.blob_size(DS.inter, DS.hidden, DS.group_size)
+    pinned = PinnedBuffer(L * E * size)
+    _fill_streaming_blobs(pinned, L, E, size)
+    host = [pinned.array[i * size:(i + 1) * size] for i in range(L * E)]
+    ptrs = [pinned.ptr + i * size for i in range(L * E)]
+    layout = moe.layout_from_blob(host[0], has_zeros=False)
+    n_slots = int(round(0.30 * L * E))
+    assert n_slots == 614
+    t = tier.ExpertTier(L, E, size, ptrs, n_slots, scratch_slots=k + 2)
+    shared = [synth.make_blob(np.random.default_rng([56, l]), DS.inter, DS.hidden, DS.group_size,
+                              expert=99999) for l in range(L)]
+    sh_dev = []
+    for b in shared:
+        d = DeviceBuffer(size + 16)
+        d.upload(b, offset=8)
+        sh_dev.append(d)
+    xs, routes, weights = synth.streaming_draw(DS, L, steps)
+    dxs = to_device(xs)
+    st = Stream()
+    ws = DeviceBuffer(moe.decode_workspace_bytes(layout, 1, k, True))
+    out32, out16 = DeviceBuffer(4 * DS.hidden), DeviceBuffer(2 * DS.hidden)
+    not_hits = 0
+    worst = 0.0
+    for step in range(steps):
+        xi = step % len(xs)
+        for l in range(L):
+            before = t.stats()
+            t.moe_decode_layer(l, sh_dev[l].ptr + 8, layout, dxs.ptr + xi * DS.hidden * 2, 1,
+                               routes[step][l], weights[step][l], ws, out32.ptr, out16.ptr,
+                               st.handle)
+            st.synchronize()
+            after = t.stats()
+            not_hits += (after["lookups"] - before["lookups"]) - \
+                (after["vram_hits"] - before["vram_hits"])
+            g32 = out32.download(np.float32, (DS.hidden,))
+            g16 = out16.download(np.float16, (DS.hidden,)).astype(np.float32)
+            want = O.moe_combine(host[l * E:(l + 1) * E], shared[l], xs[xi].astype(np.float32),
+                                 routes[step][l][0], weights[step][l][0], fast=True)
+            r, _ = assert_close(g32, want, f"step {step} layer {l} fp32")
+            assert_close(g16, want, f"step {step} layer {l} fp16")
+            worst = max(worst, r)
+        if step % 16 == 15:
+            print(f"  step {step + 1}/{steps}: {t.stats()} worst rel err {worst:.2e}", flush=True)
+    s = t.stats()
+    assert s["lookups"] == steps * L * k
+    assert s["lookups"] == s["vram_hits"] + s["ram_hits"] + s["first_touch"]
+    assert s["h2d_bytes"] == not_hits * size
+    assert s["promotions"] > 0 and s["evictions"] > 0 and s["scratch_serves"] > 0, s
+    t.close()
+    synchronize()
+    del pinned

@@ -75,7 +75,6 @@ def test_down_wait_give_up_is_reported_and_poisons():
     waiting for its unit's h' after 4 polls."""
     print("decode status: forced down-wait give-up", flush=True)
     s = _Setup(11)
-    assert moe.decode_status(s.ws) == 0
     try:
         _force(4, 1 << 20)
         got = s.given()
@@ -84,7 +83,7 @@ def test_down_wait_give_up_is_reported_and_poisons():
     st = moe.decode_status(s.ws)
     assert st & moe.DECODE_DOWN_WAIT, st
     assert np.isnan(got).all()
-    # sticky until cleared: read without clearing, then it is gone
+    # cleared by the read above
     assert moe.decode_status(s.ws) == 0
     got = s.given()
     assert moe.decode_status(s.ws) == 0

@@ -117,3 +117,21 @@ def test_host_side_validation_rejects_without_gpu_calls():
     assert lib.wisp_gpu_moe_route(fake, None, fake, 1, 512, 256, 8, 7, fake, fake, fake, None) == 1
     assert lib.wisp_gpu_expert_offsets(fake, 1, 8, 5000, fake, fake, fake, fake, None) == 1
     assert lib.wisp_gpu_topk_from_logits(fake, None, 1, 256, 65, 0, fake, fake, fake, None) == 1
+
+
+def test_header_and_reference_declarations_compile_as_c11():
+    """include/wisp_amd.h compiles as C11 with -Werror, and so does the test
+    caller that repeats the reference's launcher declarations
+    (csrc/core/wisp_engine.h:496-559) with the CUDA type names mapped to HIP:
+    C rejects an incompatible repeated declaration."""
+    inc = ["-I" + str(ROOT / "include"), "-I/opt/rocm/include", "-D__HIP_PLATFORM_AMD__"]
+    flags = ["-std=c11", "-Wall", "-Wextra", "-Werror", "-fsyntax-only"]
+    src = ROOT / "tests" / "c_abi" / "engine_call_shape.c"
+    r = subprocess.run(["gcc", *flags, *inc, str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    # a changed argument type must be caught
+    bad = src.read_text().replace("int rows, int cols, cudaStream_t s);",
+                                  "long rows, int cols, cudaStream_t s);", 1)
+    r = subprocess.run(["gcc", *flags, *inc, "-x", "c", "-"], input=bad, capture_output=True,
+                       text=True)
+    assert r.returncode != 0 and "conflicting types" in r.stderr

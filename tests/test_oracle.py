@@ -15,8 +15,8 @@ import pytest
 from oracle import oracle as O
 from wisp_amd import synth
 
-REF = O.ref()
-needs_ref = pytest.mark.skipif(REF is None, reason="reference tree not built into oracle/_ref")
+REF = O.LazyRef()   # loaded by the first test that uses it, not at import
+needs_ref = pytest.mark.skipif(not O.ref_built(), reason="reference tree not built into oracle/_ref")
 
 
 # --------------------------------------------------------------------------
@@ -375,6 +375,36 @@ def test_moe_combine_is_shared_then_rank_order():
     acc = O.expert_ffn(blobs[2], x, acc, 0.7)
     acc = O.expert_ffn(blobs[0], x, acc, 0.3)
     assert np.array_equal(got, acc)
+
+
+def test_fast_combine_matches_scalar_combine():
+    """moe_combine(fast=True), which the config-scale GPU tests use, against
+    the scalar restatement: same order (shared, then rank order), vectorised
+    dot products."""
+    rng = np.random.default_rng(31)
+    inter, hidden, gs = 256, 1024, 128
+    blobs = [synth.make_blob(rng, inter, hidden, gs, expert=e) for e in range(6)]
+    shared = synth.make_blob(rng, inter, hidden, gs, expert=99)
+    x = rng.standard_normal(hidden).astype(np.float32)
+    idx = np.array([4, -1, 1], np.int32)
+    w = np.array([0.5, 0.2, 0.3], np.float32)
+    a = O.moe_combine(blobs, shared, x, idx, w)
+    b = O.moe_combine(blobs, shared, x, idx, w, fast=True)
+    assert np.max(np.abs(a - b)) <= 1e-5 * np.max(np.abs(a))
+    c = O.moe_combine(blobs, shared, x, np.array([4, 1], np.int32), np.array([0.5, 0.3], np.float32))
+    assert np.array_equal(a, c)   # a skipped slot contributes nothing
+
+
+def test_fill_random_bytes_is_deterministic_and_uniform():
+    """The synthetic-byte generator of the config-scale tests: a pure
+    function of (seed, position), so a longer fill extends a shorter one,
+    seeds differ, and byte values are close to uniform."""
+    a = O.random_bytes(1 << 20, 7)
+    assert np.array_equal(a, O.random_bytes(1 << 20, 7))
+    assert np.array_equal(a[:1001], O.random_bytes(1001, 7))
+    assert not np.array_equal(a, O.random_bytes(1 << 20, 8))
+    h = np.bincount(a, minlength=256)
+    assert h.min() > 0.9 * (1 << 12) and h.max() < 1.1 * (1 << 12)
 
 
 @needs_ref

@@ -15,8 +15,8 @@ import pytest
 from oracle import oracle as O
 from wisp_amd import synth, tier
 
-REF = O.ref()
-needs_ref = pytest.mark.skipif(REF is None, reason="reference tree not built into oracle/_ref")
+REF = O.LazyRef()   # loaded by the first test that uses it, not at import
+needs_ref = pytest.mark.skipif(not O.ref_built(), reason="reference tree not built into oracle/_ref")
 
 
 def zipf_trace(rng, steps, n_layers, n_experts, k):

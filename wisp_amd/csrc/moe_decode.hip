@@ -85,7 +85,7 @@ struct DecodeParams {
     float* out32;         /* [M][hidden] layer output (either may be null) */
     uint16_t* out16;
     int accumulate;
-    uint32_t* status;     /* sticky DEC_STATUS_* bits of bounded waits that gave up */
+    uint32_t* status;     /* DEC_STATUS_* bits of this call's bounded waits that gave up */
     int poll_limit;       /* polls of one hand-off word or counter before giving up */
     int poll_extra;       /* added to every wait target: nonzero only to force a give-up */
 };
@@ -136,9 +136,9 @@ static inline size_t prep_lds_bytes(int mode, int n_experts, int M) {
 /* Polls of one hand-off word or counter before a wait gives up: 65,536
  * polls of 512 cycles each, about 14 ms at 2.4 GHz, so every wait ends even
  * if the workgroup it waits for never ran. A wait that gives up sets its
- * bit in the workspace's sticky status word (wisp_moe_decode_status reads
- * and clears it) and poisons what it feeds with NaN, so a broken hand-off
- * never passes for a result. */
+ * bit in the workspace's status word (cleared by the prep workgroup at the
+ * start of every call; wisp_moe_decode_status reads it) and poisons what it
+ * feeds with NaN, so a broken hand-off never passes for a result. */
 #define DEC_POLL_LIMIT (1 << 16)
 #define DEC_STATUS_ROUTER_WAIT 1u   /* prep: router logits never arrived  */
 #define DEC_STATUS_DOWN_WAIT 2u     /* down wave: h' of its unit never completed */
@@ -259,6 +259,10 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
         return;
     }
 
+    /* this call's status starts clear (the down waits of the next launch
+     * and the routing wait below set bits) */
+    if (threadIdx.x == 0)
+        __hip_atomic_store(P.status, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (int e = threadIdx.x; e < n_experts; e += blockDim.x) s_tab[e] = (const uint8_t*)table[e];
     for (int i = threadIdx.x; i < P.hidden / 16; i += blockDim.x) P.tile_cnt[i] = 0;
     for (int i = threadIdx.x; i < P.max_u * P.upe; i += blockDim.x) P.hcnt[i * DEC_HCNT_STRIDE] = 0;

@@ -145,8 +145,8 @@ DECODE_DOWN_WAIT = 2
 
 
 def decode_status(ws: DeviceBuffer | None, stream: int = 0, clear: bool = True) -> int:
-    """Sticky status bits of the bounded waits of decode calls on `ws`
-    (waits for `stream`); 0 when every wait completed."""
+    """Status bits of the bounded waits of the most recent decode call on
+    `ws`; waits for `stream`; 0 when every wait completed."""
     flags = ctypes.c_uint32(0)
     rc = lib().wisp_moe_decode_status(ws.ptr if ws is not None else None, stream or None,
                                       ctypes.byref(flags), 1 if clear else 0)

@@ -149,3 +149,48 @@ def slot_stride(inter: int, hidden: int, gs: int) -> int:
     that every section (120 + 16k bytes into the blob) is 16-byte aligned."""
     b = blob_size(inter, hidden, gs) + 8
     return (b + 4095) // 4096 * 4096
+
+
+# Seeds of the benchmark workloads (the config-scale tests reuse them).
+PREFILL_SEED = 2048
+DSV3_BENCH_SEED = 777
+MIXTRAL_BENCH_SEED = 1234
+
+
+def bench_expert(shape: MoeShape, seed: int, set_idx: int, e: int,
+                 out: np.ndarray | None = None) -> np.ndarray:
+    """Routed expert e of benchmark expert set set_idx."""
+    return make_blob(np.random.default_rng([seed, set_idx, e]), shape.inter, shape.hidden,
+                     shape.group_size, expert=e, out=out)
+
+
+def bench_shared(shape: MoeShape, seed: int, set_idx: int,
+                 out: np.ndarray | None = None) -> np.ndarray:
+    """The shared expert of benchmark set set_idx."""
+    return make_blob(np.random.default_rng([seed, 99999, set_idx]), shape.inter, shape.hidden,
+                     shape.group_size, expert=99999, out=out)
+
+
+def prefill_draw(shape: MoeShape, n_tokens: int, seed: int = PREFILL_SEED):
+    """The prefill workload's inputs: top-k routing drawn without replacement
+    from Zipf(1.1) over the routed experts, positive weights summing to 1,
+    and fp16 N(0, 1) tokens, in that order from one generator."""
+    rng = np.random.default_rng(seed)
+    idx = zipf_topk(rng, n_tokens, shape.n_experts, shape.top_k)
+    w = route_weights(rng, n_tokens, shape.top_k)
+    x = make_x(rng, n_tokens, shape.hidden)
+    return idx, w, x
+
+
+def streaming_draw(shape: MoeShape, n_layers: int, steps: int, seed: int = 55, n_x: int = 16):
+    """The expert-streaming workload's inputs: a pool of n_x fp16 tokens, then
+    per step and layer one token's Zipf(1.1) top-k routing and weights.
+    Returns (x [n_x, hidden], routes[step][layer] [1, top_k],
+    weights[step][layer] [1, top_k])."""
+    rng = np.random.default_rng(seed)
+    xs = make_x(rng, n_x, shape.hidden)
+    routes = [[zipf_topk(rng, 1, shape.n_experts, shape.top_k) for _ in range(n_layers)]
+              for _ in range(steps)]
+    weights = [[route_weights(rng, 1, shape.top_k) for _ in range(n_layers)]
+               for _ in range(steps)]
+    return xs, routes, weights
