@@ -224,8 +224,9 @@ enum {
 /* Waits for stream s, then returns in *flags the status bits of the most
  * recent decode call on d_workspace (0: every wait of that call completed;
  * each call starts from 0, so check after every call that matters), and
- * clears them when clear != 0. Undefined before the first call.
- * Synchronous. */
+ * clears them when clear != 0. Undefined before the first call. d_workspace
+ * NULL: the static workspace of wisp_gpu_moe_layer_decode_int4_noalloc on
+ * the device of s. Synchronous. */
 hipError_t wisp_moe_decode_status(void* d_workspace, hipStream_t s,
                                   uint32_t* flags, int clear);
 
@@ -276,6 +277,31 @@ hipError_t wisp_gpu_moe_layer_decode_int4(const wisp_half* d_router_w,
                                           size_t workspace_bytes,
                                           int accumulate, float* d_out_f32,
                                           wisp_half* d_out_f16, hipStream_t s);
+
+/* Bytes of the static workspace of wisp_gpu_moe_layer_decode_int4_noalloc
+ * (one per device, held until the process ends). */
+#define WISP_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): wisp_gpu_moe_layer_decode_int4 without the workspace
+ * arguments. Its workspace is a library-owned static device array of
+ * WISP_NOALLOC_SCRATCH_BYTES per device; the call allocates nothing.
+ * Returns hipErrorInvalidValue, before any launch, when the layer's
+ * workspace (wisp_moe_decode_workspace_bytes) would exceed that size: it
+ * fits DeepSeek-V3 (hidden 7168, inter 2048, top-8 + shared) and
+ * Mixtral-8x7B (hidden 4096, inter 14336, top-2) layers for 1..4 tokens.
+ * Every call on a device shares the one array, so calls that overlap on a
+ * device (two streams, two host threads) race: issue them in one stream
+ * order. The status word of wisp_moe_decode_status is that array's
+ * (d_workspace = NULL). */
+hipError_t wisp_gpu_moe_layer_decode_int4_noalloc(
+    const wisp_half* d_router_w, const wisp_half* d_router_bias,
+    int router_kind, float* d_scores, int* d_topk_idx, float* d_topk_w,
+    const void* const* d_expert_table, const void* d_shared_blob,
+    const WispExpertLayout* L, const void* d_x, int x_dtype, int n_tokens,
+    int top_k, int n_experts, int accumulate, float* d_out_f32,
+    wisp_half* d_out_f16, hipStream_t s);
 
 /* ======================================================================= *
  * 5. Fused int4 MoE prefill (grouped GEMM over routed token tiles)

@@ -53,6 +53,9 @@ _SIGS = {
                                                P, c_int, c_int, c_int, c_int, P, c_size_t, c_int,
                                                P, P, P]),
     "wisp_moe_decode_status": (c_int, [P, P, P, c_int]),
+    "wisp_gpu_moe_layer_decode_int4_noalloc": (c_int, [P, P, c_int, P, P, P, P, P,
+                                                       POINTER(WispExpertLayout), P, c_int, c_int,
+                                                       c_int, c_int, c_int, P, P, P]),
     # section 5: fused prefill
     "wisp_moe_prefill_workspace_bytes": (c_size_t, [POINTER(WispExpertLayout), c_int, c_int, c_int,
                                                     c_int]),

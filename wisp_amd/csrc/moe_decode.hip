@@ -50,6 +50,8 @@
  */
 #include "route_common.h"
 
+#include <mutex>
+
 #define DEC_MAX_TOKENS 4
 #define DEC_MAX_TOPK 64
 #define DEC_MAX_WAVES 8
@@ -1453,12 +1455,84 @@ extern "C" hipError_t wisp_gpu_moe_layer_decode_int4(
                      d_workspace, workspace_bytes, accumulate, d_out_f32, d_out_f16, s);
 }
 
+/* ---- the layer entry point that allocates nothing -----------------------
+ * Its workspace is this file-scope device array: one copy per device, held
+ * until the process ends. In host code `scratch` only names the symbol;
+ * its device address comes from hipGetSymbolAddress, once per device, with
+ * that device current, and only that address is handed to kernels and
+ * copies. Every call on a device shares the array and leaves its contents
+ * behind: the prep kernel zeroes the counters each call needs, and the
+ * routing epoch and words are built to persist (a zero-filled array is a
+ * valid start). Calls that overlap on one device race. */
+#define WISP_NOALLOC_MAX_DEVICES 64
+static __device__ __align__(256) uint8_t scratch[WISP_NOALLOC_SCRATCH_BYTES];
+static void* g_scratch_ptr[WISP_NOALLOC_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+/* Device address of `scratch` on the device of stream s (the current device
+ * for the null stream). */
+static hipError_t noalloc_scratch(hipStream_t s, void** out) {
+    int dev = 0;
+    hipError_t e = hipSuccess;
+    if (s) {
+        dev = hipGetStreamDeviceId(s);
+        if (dev < 0) return hipErrorInvalidResourceHandle;
+    } else {
+        e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+    }
+    if (dev >= WISP_NOALLOC_MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        int cur = 0;
+        e = hipGetDevice(&cur);
+        if (e != hipSuccess) return e;
+        if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) (void)hipSetDevice(cur);
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+
+extern "C" hipError_t wisp_gpu_moe_layer_decode_int4_noalloc(
+    const wisp_half* d_router_w, const wisp_half* d_router_bias, int router_kind,
+    float* d_scores, int* d_topk_idx, float* d_topk_w, const void* const* d_expert_table,
+    const void* d_shared_blob, const WispExpertLayout* L, const void* d_x, int x_dtype,
+    int n_tokens, int top_k, int n_experts, int accumulate, float* d_out_f32,
+    wisp_half* d_out_f16, hipStream_t s) {
+    const void* any = (const void*)1;   /* the workspace is checked below */
+    if (!decode_args_ok(d_expert_table, d_x, x_dtype, n_tokens, top_k, n_experts, any, d_out_f32,
+                        d_out_f16) ||
+        !layer_args_ok(d_router_w, router_kind, d_scores, d_topk_idx, d_topk_w, top_k, n_experts,
+                       L))
+        return hipErrorInvalidValue;
+    const size_t need = ws_layout(L, n_tokens, top_k, d_shared_blob != nullptr).total;
+    if (need > WISP_NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;
+    void* ws = nullptr;
+    hipError_t e = noalloc_scratch(s, &ws);
+    if (e != hipSuccess) return e;
+    return layer_run(d_router_w, d_router_bias, router_kind, d_scores, d_topk_idx, d_topk_w,
+                     d_expert_table, d_shared_blob, L, d_x, x_dtype, n_tokens, top_k, n_experts, ws,
+                     WISP_NOALLOC_SCRATCH_BYTES, accumulate, d_out_f32, d_out_f16, s);
+}
+
 extern "C" hipError_t wisp_moe_decode_status(void* d_workspace, hipStream_t s, uint32_t* flags,
                                              int clear) {
     if (!flags) return hipErrorInvalidValue;
     *flags = 0;
     char* ws = (char*)d_workspace;
-    if (!ws) return hipErrorInvalidValue;
+    if (!ws) {
+        /* the static workspace of wisp_gpu_moe_layer_decode_int4_noalloc */
+        void* p = nullptr;
+        hipError_t e = noalloc_scratch(s, &p);
+        if (e != hipSuccess) return e;
+        ws = (char*)p;
+    }
     hipError_t e = hipStreamSynchronize(s);
     if (e != hipSuccess) return e;
     uint32_t v = 0;

@@ -146,7 +146,8 @@ DECODE_DOWN_WAIT = 2
 
 def decode_status(ws: DeviceBuffer | None, stream: int = 0, clear: bool = True) -> int:
     """Status bits of the bounded waits of the most recent decode call on
-    `ws`; waits for `stream`; 0 when every wait completed."""
+    `ws` (None: the no-alloc entry point's static workspace); waits for
+    `stream`; 0 when every wait completed."""
     flags = ctypes.c_uint32(0)
     rc = lib().wisp_moe_decode_status(ws.ptr if ws is not None else None, stream or None,
                                       ctypes.byref(flags), 1 if clear else 0)
