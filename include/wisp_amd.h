@@ -449,6 +449,82 @@ hipError_t wisp_tier_moe_decode_layer(WispExpertTier* t, int layer,
                                       hipStream_t compute);
 
 /* ======================================================================= *
+ * 7. Real-weight ingestion (host only)
+ *
+ *    The converter's group-wise int4 quantizer and the expert file format,
+ *    so real checkpoints become the blobs the kernels read, and the reader
+ *    that brings a blob file into (pinned) host memory for the tiers.
+ * ======================================================================= */
+
+enum { WISP_WEIGHT_F32 = 0, WISP_WEIGHT_F16 = 1, WISP_WEIGHT_BF16 = 2 };
+
+/* Group-wise asymmetric int4 quantization of a row-major [rows, cols]
+ * matrix, byte-identical to the reference converter's quantize_int4
+ * (wisp/converter/quantizer.py:46-86): per group of group_size consecutive
+ * elements (the last one padded with the last element), zero = (max + min)
+ * / 2, scale = max((max - min) / 15, 1e-8) in fp32, q = clamp(round half to
+ * even((x - zero) / scale) + 8, 0, 15), packed two per byte (low nibble =
+ * even element; an odd count leaves the last high nibble 0); scale and zero
+ * stored as fp16 (round to nearest even). w is fp32, fp16 or bf16 per dtype
+ * (WISP_WEIGHT_*). packed holds ceil(n/2) bytes, scales and zeros
+ * ceil(n/group_size) entries each. Returns 0, -1 for bad arguments, -2 for
+ * a non-finite weight (the reference would write meaningless nibbles). */
+int wisp_quantize_int4(const void* w, int dtype, uint32_t rows, uint32_t cols,
+                       uint32_t group_size, uint8_t* packed, wisp_half* scales,
+                       wisp_half* zeros);
+
+/* Bytes of an expert blob with matrices rows[m] x cols[m] (gate, up, down):
+ * the 120-byte header plus [packed][scales][zeros] per matrix. 0 for bad
+ * arguments. */
+size_t wisp_expert_blob_bytes(const uint32_t rows[3], const uint32_t cols[3],
+                              uint32_t group_size);
+
+/* Writes an expert blob (the reference file format, wisp/converter/
+ * partitioner.py:56-89) into dst. Returns the bytes written, or 0 when
+ * capacity is too small or an argument is bad. */
+size_t wisp_expert_blob_write(void* dst, size_t capacity, uint32_t layer,
+                              uint32_t expert, uint32_t group_size,
+                              const uint32_t rows[3], const uint32_t cols[3],
+                              const uint8_t* const packed[3],
+                              const wisp_half* const scales[3],
+                              const wisp_half* const zeros[3]);
+
+/* Quantizes one expert (gate and up [inter, hidden], down [hidden, inter],
+ * each row-major in dtype) and writes its blob into dst: the converter's
+ * per-expert path (wisp/converter/partitioner.py:160-180 quantizes each
+ * projection, :56-89 writes the file). Returns the blob bytes, 0 on error. */
+size_t wisp_expert_quantize_blob(const void* gate, const void* up,
+                                 const void* down, int dtype, uint32_t inter,
+                                 uint32_t hidden, uint32_t group_size,
+                                 uint32_t layer, uint32_t expert, void* dst,
+                                 size_t capacity);
+
+/* Error codes of the expert file functions. */
+enum {
+    WISP_IO_BAD_ARGUMENT = -1,
+    WISP_IO_MISSING = -2,       /* cannot open the file                     */
+    WISP_IO_TOO_LARGE = -3,     /* empty, or larger than the destination     */
+    WISP_IO_SHORT_READ = -4     /* read or write ended early                 */
+};
+
+/* out = "<model_path>/experts/L%03u_E%05u.bin" (wisp/converter/manifest.py
+ * expert_filename). Returns 0, or -1 when it does not fit. */
+int wisp_expert_file_path(char* out, size_t capacity, const char* model_path,
+                          uint32_t layer, uint32_t expert);
+
+/* Reads a whole expert file into dst (max_bytes), as read_expert_ssd does
+ * (csrc/core/wisp_engine.c:351-380). Returns the bytes read (> 0) or a
+ * WISP_IO_* code. */
+int64_t wisp_expert_file_read(const char* model_path, uint32_t layer,
+                              uint32_t expert, void* dst, size_t max_bytes);
+
+/* Writes a blob to its expert file through a temporary file and a rename
+ * (wisp/converter/partitioner.py:79-89). The experts/ directory must exist.
+ * Returns 0 or a WISP_IO_* code. */
+int wisp_expert_file_write(const char* model_path, uint32_t layer,
+                           uint32_t expert, const void* blob, size_t bytes);
+
+/* ======================================================================= *
  * 9. Profiling hook
  * ======================================================================= */
 

@@ -1,0 +1,109 @@
+"""GPU: MoE layers over experts that went through the real-weight path:
+checkpoint-like fp16 projections quantized by the converter restatement
+(wisp_expert_quantize_blob, byte-identical to the reference's quantize_int4,
+so zero points are nonzero), written as expert files, read back with
+wisp_expert_file_read into pinned host memory, then served by the fused
+decode (router included) and the prefill against the oracle.
+
+The activations include a large-magnitude case (x scaled by 24, so
+|h| = |silu(g) u| reaches a few thousand and the layer output a few
+hundred): h' is kept in fp16 between the two projections, which holds
+|h| < 65504; this case pins the behaviour well inside that range."""
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.gpu_util import assert_close
+from wisp_amd import ingest, moe, synth
+from wisp_amd.hip import DeviceBuffer, PinnedBuffer, synchronize, to_device
+
+pytestmark = pytest.mark.gpu
+
+
+def _model_dir(tmp_path, n_exp, inter, hidden, gs, seed):
+    """Writes experts/L000_E*.bin (experts 0..n_exp-1, shared = n_exp)."""
+    rng = np.random.default_rng(seed)
+    os.makedirs(tmp_path / "experts")
+    for e in range(n_exp + 1):
+        gate = (rng.standard_normal((inter, hidden)) * 0.02).astype(np.float16)
+        up = (rng.standard_normal((inter, hidden)) * 0.02).astype(np.float16)
+        down = (rng.standard_normal((hidden, inter)) * 0.02).astype(np.float16)
+        blob = ingest.quantize_expert_blob(gate, up, down, gs, layer=0, expert=e)
+        ingest.write_expert_file(str(tmp_path), 0, e, blob)
+    return synth.blob_size(inter, hidden, gs)
+
+
+@pytest.mark.parametrize("hidden,inter,n_exp,top_k,kind", [
+    (7168, 2048, 16, 8, moe.ROUTER_SIGMOID),      # DeepSeek-V3 expert shape
+    (4096, 1024, 8, 2, moe.ROUTER_SOFTMAX),
+])
+def test_decode_layer_on_quantized_files(tmp_path, hidden, inter, n_exp, top_k, kind):
+    print(f"real weights: hidden {hidden} inter {inter}, {n_exp} experts + shared", flush=True)
+    gs = 128
+    size = _model_dir(tmp_path, n_exp, inter, hidden, gs, seed=hidden + n_exp)
+    pinned = PinnedBuffer((n_exp + 1) * size)
+    for e in range(n_exp + 1):
+        got = ingest.read_expert_file(str(tmp_path), 0, e, pinned.ptr + e * size, size)
+        assert got == size
+    blobs = [pinned.array[e * size:(e + 1) * size] for e in range(n_exp + 1)]
+    arena = moe.ExpertArena(n_exp, inter, hidden, gs, lambda e, out: blobs[e], has_zeros=True)
+    assert arena.layout.has_zeros == 1
+    sh = DeviceBuffer(size + 16)
+    sh.upload(blobs[n_exp], offset=8)
+    rng = np.random.default_rng(5)
+    W = synth.make_router(rng, n_exp, hidden, std=0.05)
+    dW = to_device(W)
+    rkind = "softmax" if kind == moe.ROUTER_SOFTMAX else "sigmoid"
+    for M, scale in ((1, 1.0), (3, 1.0), (1, 24.0)):
+        x = (synth.make_x(rng, M, hidden).astype(np.float32) * scale).astype(np.float16)
+        dx = to_device(x)
+        scores = DeviceBuffer(4 * M * n_exp)
+        idx, w = DeviceBuffer(4 * M * top_k), DeviceBuffer(4 * M * top_k)
+        out = DeviceBuffer(4 * M * hidden)
+        ws = DeviceBuffer(moe.decode_workspace_bytes(arena.layout, M, top_k, True))
+        moe.moe_layer_decode_int4(dW.ptr, 0, kind, scores.ptr, idx.ptr, w.ptr, arena.table.ptr,
+                                  sh.ptr + 8, arena.layout, dx.ptr, M, top_k, n_exp, ws,
+                                  out32=out.ptr)
+        synchronize()
+        assert moe.decode_status(ws) == 0
+        g = out.download(np.float32, (M, hidden))
+        gi = idx.download(np.int32, (M, top_k))
+        for t in range(M):
+            oi, ow, _ = O.router_topk(W.view(np.uint16), None, x[t].astype(np.float32), top_k,
+                                      kind=rkind)
+            assert gi[t].tolist() == oi.tolist(), (gi[t], oi)
+            want = O.moe_combine(blobs[:n_exp], blobs[n_exp], x[t].astype(np.float32), oi, ow,
+                                 fast=True)
+            r, c = assert_close(g[t], want, f"M={M} x*{scale} token {t}")
+            print(f"  M={M} x*{scale} token {t}: max-rel-err {r:.2e} cos {c:.6f} "
+                  f"max|out| {np.abs(want).max():.1f}", flush=True)
+
+
+def test_prefill_on_quantized_files(tmp_path):
+    print("real weights: prefill, 200 tokens", flush=True)
+    hidden, inter, n_exp, top_k, gs, T = 2048, 512, 8, 2, 128, 200
+    size = _model_dir(tmp_path, n_exp, inter, hidden, gs, seed=77)
+    host = np.empty((n_exp + 1) * size, np.uint8)
+    for e in range(n_exp + 1):
+        ingest.read_expert_file(str(tmp_path), 0, e, host.ctypes.data + e * size, size)
+    blobs = [host[e * size:(e + 1) * size] for e in range(n_exp + 1)]
+    arena = moe.ExpertArena(n_exp, inter, hidden, gs, lambda e, out: blobs[e], has_zeros=True)
+    sh = DeviceBuffer(size + 16)
+    sh.upload(blobs[n_exp], offset=8)
+    rng = np.random.default_rng(8)
+    idx = synth.zipf_topk(rng, T, n_exp, top_k)
+    w = synth.route_weights(rng, T, top_k)
+    x = synth.make_x(rng, T, hidden)
+    dx, di, dw = to_device(x), to_device(idx), to_device(w)
+    ws = DeviceBuffer(moe.prefill_workspace_bytes(arena.layout, T, top_k, n_exp, True))
+    out = DeviceBuffer(4 * T * hidden)
+    moe.moe_prefill_int4(arena.table.ptr, sh.ptr + 8, arena.layout, dx.ptr, T, di.ptr, dw.ptr,
+                         top_k, n_exp, ws, out32=out.ptr)
+    synchronize()
+    g = out.download(np.float32, (T, hidden))
+    for t in (0, 1, 99, 150, 199):
+        want = O.moe_combine(blobs[:n_exp], blobs[n_exp], x[t].astype(np.float32), idx[t], w[t],
+                             fast=True)
+        assert_close(g[t], want, f"prefill token {t}")

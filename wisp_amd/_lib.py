@@ -76,6 +76,16 @@ _SIGS = {
     "wisp_tier_stats": (None, [P, P]),
     "wisp_tier_moe_decode_layer": (c_int, [P, c_int, P, POINTER(WispExpertLayout), P, c_int, c_int,
                                            P, P, c_int, P, c_size_t, P, P, P]),
+    # section 7: real-weight ingestion
+    "wisp_quantize_int4": (c_int, [P, c_int, c_uint32, c_uint32, c_uint32, P, P, P]),
+    "wisp_expert_blob_bytes": (c_size_t, [P, P, c_uint32]),
+    "wisp_expert_blob_write": (c_size_t, [P, c_size_t, c_uint32, c_uint32, c_uint32, P, P, P, P,
+                                          P]),
+    "wisp_expert_quantize_blob": (c_size_t, [P, P, P, c_int, c_uint32, c_uint32, c_uint32,
+                                             c_uint32, c_uint32, P, c_size_t]),
+    "wisp_expert_file_path": (c_int, [P, c_size_t, c_char_p, c_uint32, c_uint32]),
+    "wisp_expert_file_read": (ctypes.c_int64, [c_char_p, c_uint32, c_uint32, P, c_size_t]),
+    "wisp_expert_file_write": (c_int, [c_char_p, c_uint32, c_uint32, P, c_size_t]),
     # profiling
     "wisp_amd_set_kernel_events": (None, [P, c_int]),
     # internal test hook (not in the header): bounded-wait poll limit and target offset
