@@ -5,10 +5,12 @@ so zero points are nonzero), written as expert files, read back with
 wisp_expert_file_read into pinned host memory, then served by the fused
 decode (router included) and the prefill against the oracle.
 
-The activations include a large-magnitude case (x scaled by 24, so
+The activations include a large-magnitude case (x scaled by 20, so
 |h| = |silu(g) u| reaches a few thousand and the layer output a few
 hundred): h' is kept in fp16 between the two projections, which holds
-|h| < 65504; this case pins the behaviour well inside that range."""
+|h| < 65504; this case pins the behaviour well inside that range. Its
+sigmoid router saturates: five experts score exactly 1 in fp32 and must be
+taken lowest index first, as the oracle takes them."""
 import os
 
 import numpy as np
@@ -20,6 +22,24 @@ from wisp_amd import ingest, moe, synth
 from wisp_amd.hip import DeviceBuffer, PinnedBuffer, synchronize, to_device
 
 pytestmark = pytest.mark.gpu
+
+
+def _decided(W, x, k, kind):
+    """True when the top-k selection cannot depend on fp32 rounding: no two
+    of the k + 1 largest float64 keys closer than 2e-5 of the largest, except
+    sigmoid scores that are exactly 1 in fp32 for certain (logit >= 17.5;
+    exp(-l) < 2^-25 there), which tie and go to the lowest index."""
+    l = W.astype(np.float64) @ x.astype(np.float64)
+    if kind == "softmax":
+        key = l
+    else:
+        key = np.where(l >= 17.5, 1.0, 1.0 / (1.0 + np.exp(-l)))
+        if np.any((l >= 15.5) & (l < 17.5)):
+            return False          # the fp32 score may or may not have saturated
+    srt = np.sort(key)[::-1][: k + 1]
+    d = np.abs(np.diff(srt))
+    tol = 2e-5 * max(np.max(np.abs(srt)), 1.0)
+    return not np.any((d > 0) & (d <= tol))
 
 
 def _model_dir(tmp_path, n_exp, inter, hidden, gs, seed):
@@ -56,7 +76,7 @@ def test_decode_layer_on_quantized_files(tmp_path, hidden, inter, n_exp, top_k, 
     W = synth.make_router(rng, n_exp, hidden, std=0.05)
     dW = to_device(W)
     rkind = "softmax" if kind == moe.ROUTER_SOFTMAX else "sigmoid"
-    for M, scale in ((1, 1.0), (3, 1.0), (1, 24.0)):
+    for M, scale in ((1, 1.0), (3, 1.0), (1, 20.0)):
         x = (synth.make_x(rng, M, hidden).astype(np.float32) * scale).astype(np.float16)
         dx = to_device(x)
         scores = DeviceBuffer(4 * M * n_exp)
@@ -70,10 +90,16 @@ def test_decode_layer_on_quantized_files(tmp_path, hidden, inter, n_exp, top_k, 
         assert moe.decode_status(ws) == 0
         g = out.download(np.float32, (M, hidden))
         gi = idx.download(np.int32, (M, top_k))
+        gw = w.download(np.float32, (M, top_k))
         for t in range(M):
             oi, ow, _ = O.router_topk(W.view(np.uint16), None, x[t].astype(np.float32), top_k,
                                       kind=rkind)
-            assert gi[t].tolist() == oi.tolist(), (gi[t], oi)
+            if _decided(W, x[t], top_k, rkind):
+                assert gi[t].tolist() == oi.tolist(), (gi[t], oi)
+            else:   # fp32 summation order may decide it: check the device's own choice
+                print(f"  M={M} x*{scale} token {t}: near-tie, device selection {gi[t]}")
+                assert scale == 1.0, "the large-activation case must pin the saturated ties"
+                oi, ow = gi[t], gw[t]
             want = O.moe_combine(blobs[:n_exp], blobs[n_exp], x[t].astype(np.float32), oi, ow,
                                  fast=True)
             r, c = assert_close(g[t], want, f"M={M} x*{scale} token {t}")

@@ -4,9 +4,11 @@
  *
  * Selection rule (csrc/core/wisp_engine.c:803-815, csrc/cuda/router.cu:
  * 118-130): k passes of "largest untaken score wins, ties to the lowest
- * index". Softmax and sigmoid are strictly increasing, so the selection
- * runs on the logit itself (plus bias where it enters before the
- * activation).
+ * index". The softmax selection runs on the logit (plus bias): exp is
+ * increasing, and distinct logits give equal probabilities only at
+ * near-ties. The sigmoid selection runs on the fp32 score (plus bias, if
+ * any), which saturates to 1 for logits above about 16.6: saturated experts
+ * tie and go to the lowest index, as the oracle's do.
  */
 #pragma once
 
@@ -242,8 +244,11 @@ __device__ __forceinline__ void topk_wave_small(const float* lg, const uint16_t*
     const int lane = threadIdx.x & 63;
     const bool act = lane < n_experts;
     const float l = act ? lg[lane] : -INFINITY;
+    /* sigmoid: select on the score itself (it saturates to 1 in fp32, and
+     * saturated experts tie, lowest index first, as in the oracle) */
     float key = l;
-    if (act && sig && bias) key = 1.0f / (1.0f + __expf(-l)) + half_bits_to_float(bias[lane]);
+    if (act && sig)
+        key = 1.0f / (1.0f + __expf(-l)) + (bias ? half_bits_to_float(bias[lane]) : 0.0f);
     const uint64_t ce = act ? route_composite(key, lane) : 0ull;
     s_key[lane] = ce;
     const float mx = wave_max_dpp(l);
@@ -379,7 +384,7 @@ __device__ __forceinline__ void topk_block(const float* lg, const uint16_t* __re
     for (int e = tid; e < n_experts; e += nt) {
         const float l = lg[e];
         float k = l;
-        if (sig && bias) k = 1.0f / (1.0f + __expf(-l)) + half_bits_to_float(bias[e]);
+        if (sig) k = 1.0f / (1.0f + __expf(-l)) + (bias ? half_bits_to_float(bias[e]) : 0.0f);
         s_ck[e] = route_composite(k, e);
         s_sc[e] = l;
         mx = fmaxf(mx, l);
