@@ -84,6 +84,28 @@ void wisp_gpu_swiglu_ffn(const wisp_half* Wg, const wisp_half* Wu,
 void wisp_gpu_scale_accum(float* acc, const float* x, float w, int n,
                           hipStream_t s);
 
+/* y = W^T x; fp16 W [rows, cols], fp32 x [rows], y [cols]. Early-returns on
+ * rows <= 0 or cols <= 0. Replaces csrc/cuda/matmul.cu:67-89
+ * (csrc/core/wisp_engine.h:501-502). */
+void wisp_gpu_gemv_t_f16(const wisp_half* W, const float* x, float* y,
+                         int rows, int cols, hipStream_t s);
+
+/* y = x / sqrt(mean(x^2) + eps) * w over n elements (fp32 x/y, fp16 w;
+ * y may alias x). Early-returns on n <= 0. Replaces
+ * csrc/cuda/matmul.cu:92-121 (csrc/core/wisp_engine.h:503-504). */
+void wisp_gpu_rmsnorm(const float* x, const wisp_half* w, float* y,
+                      int n, float eps, hipStream_t s);
+
+/* x[i] += delta[i]. Early-returns on n <= 0. Replaces
+ * csrc/cuda/matmul.cu:124-134 (csrc/core/wisp_engine.h:505-506). */
+void wisp_gpu_residual_add(float* x, const float* delta, int n,
+                           hipStream_t s);
+
+/* out[i] = silu(gate[i]) * up[i]. Early-returns on n <= 0. Replaces
+ * csrc/cuda/matmul.cu:136-148 (csrc/core/wisp_engine.h:507-508). */
+void wisp_gpu_swiglu(const float* gate, const float* up, float* out, int n,
+                     hipStream_t s);
+
 /* logits = W x + bias (fp16 W/bias, fp32 x), softmax, top-k (ties to the
  * lowest index), renormalised weights. out_idx/out_w are HOST pointers
  * (pinned for true asynchrony) filled by async D2H on `s`; the caller
@@ -302,6 +324,39 @@ hipError_t wisp_gpu_moe_layer_decode_int4_noalloc(
     const WispExpertLayout* L, const void* d_x, int x_dtype, int n_tokens,
     int top_k, int n_experts, int accumulate, float* d_out_f32,
     wisp_half* d_out_f16, hipStream_t s);
+
+/* ---- the FFN half of a decode step ---------------------------------------
+ *
+ * For a MoE layer, decode_step runs (csrc/core/wisp_engine.c:1718-1722)
+ *     norm = RMSNorm(x) * post_norm;  ffn = MoE(norm);  x += ffn
+ * wisp_gpu_moe_block_int4 does all three for n_tokens rows of the fp32
+ * residual stream x [n_tokens][hidden] (updated in place), so the engine's
+ * op_rmsnorm / run_moe / op_residual sequence becomes one call per layer.
+ * Any n_tokens: up to 4 rows (decode, speculative verify of up to 4
+ * drafted tokens) use the fused decode (the router in fp32 on the
+ * normalised rows, then wisp_gpu_moe_layer_decode_int4 accumulating into
+ * x); more rows (prefill, longer verify batches) route on fp16 normalised
+ * rows (wisp_gpu_moe_route) and run the grouped GEMM
+ * (wisp_gpu_moe_prefill_int4) accumulating into x, one pass over the
+ * experts for all rows instead of the reference's per-token decode_step
+ * loop (csrc/core/wisp_engine.c:2292-2307, 2317-2330). The routing of every
+ * row lands in d_scores / d_topk_idx / d_topk_w as in the layer call.
+ * Needs hidden % 256 == 0 and a 16-byte aligned x for more than 4 rows.
+ * The workspace (wisp_moe_block_workspace_bytes for the largest n_tokens
+ * used) is dedicated to this call and may be shared by calls of different
+ * n_tokens, one at a time; it needs no zeroing. */
+size_t wisp_moe_block_workspace_bytes(const WispExpertLayout* L, int n_tokens,
+                                      int top_k, int n_experts, int has_shared);
+hipError_t wisp_gpu_moe_block_int4(float* d_x, const wisp_half* d_post_norm_w,
+                                   float eps, const wisp_half* d_router_w,
+                                   const wisp_half* d_router_bias,
+                                   int router_kind, float* d_scores,
+                                   int* d_topk_idx, float* d_topk_w,
+                                   const void* const* d_expert_table,
+                                   const void* d_shared_blob,
+                                   const WispExpertLayout* L, int n_tokens,
+                                   int top_k, int n_experts, void* d_workspace,
+                                   size_t workspace_bytes, hipStream_t s);
 
 /* ======================================================================= *
  * 5. Fused int4 MoE prefill (grouped GEMM over routed token tiles)

@@ -52,6 +52,9 @@ def orc():
         h.orc_gemv_int4_f64.argtypes = [c_void_p] * 5 + [c_int] * 3
         h.orc_gemv_f16.argtypes = [c_void_p] * 3 + [c_int] * 2
         h.orc_swiglu.argtypes = [c_void_p] * 3 + [c_int]
+        h.orc_gemv_t_f16.argtypes = [c_void_p] * 3 + [c_int] * 2
+        h.orc_rmsnorm.argtypes = [c_void_p] * 3 + [c_int, c_float]
+        h.orc_residual_add.argtypes = [c_void_p, c_void_p, c_int]
         h.orc_scale_accum.argtypes = [c_void_p, c_void_p, c_float, c_int]
         h.orc_expert_ffn.argtypes = [c_void_p] * 4 + [c_float, c_void_p]
         h.orc_expert_ffn_fast.argtypes = [c_void_p] * 4 + [c_float, c_void_p]
@@ -92,6 +95,9 @@ def ref():
         h.ref_gemv_int4.argtypes = [c_void_p] * 5 + [c_int] * 3
         h.ref_gemv_f16.argtypes = [c_void_p] * 3 + [c_int] * 2
         h.ref_swiglu.argtypes = [c_void_p] * 3 + [c_int]
+        h.ref_gemv_t_f16.argtypes = [c_void_p] * 3 + [c_int] * 2
+        h.ref_rmsnorm.argtypes = [c_void_p] * 3 + [c_int, c_float]
+        h.ref_residual_add.argtypes = [c_void_p, c_void_p, c_int]
         h.ref_router_topk.argtypes = [c_void_p] * 4 + [c_int] * 3 + [c_void_p] * 2
         h.ref_half_to_float.restype = c_float
         h.ref_half_to_float.argtypes = [c_uint16]
@@ -231,4 +237,25 @@ def dequant_f32(packed, scales, zeros, n, gs) -> np.ndarray:
 def random_bytes(n: int, seed: int) -> np.ndarray:
     out = np.empty(n, np.uint8)
     orc().orc_fill_random_bytes(_p(out), n, seed)
+    return out
+
+
+def gemv_t_f16(W, x):
+    rows, cols = W.shape
+    y = np.empty(cols, np.float32)
+    orc().orc_gemv_t_f16(_p(np.ascontiguousarray(W)), _p(np.ascontiguousarray(x, dtype=np.float32)),
+                         _p(y), rows, cols)
+    return y
+
+
+def rmsnorm(x, w, eps):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    orc().orc_rmsnorm(_p(x), _p(np.ascontiguousarray(w)), _p(y), x.size, float(eps))
+    return y
+
+
+def residual_add(x, d):
+    out = np.array(x, dtype=np.float32, copy=True)
+    orc().orc_residual_add(_p(out), _p(np.ascontiguousarray(d, dtype=np.float32)), out.size)
     return out

@@ -15,6 +15,9 @@
  *   cpu_gemv_int4        csrc/core/wisp_engine.c:822-845
  *   cpu_gemv_f16         csrc/core/wisp_engine.c:630-645
  *   cpu_swiglu           csrc/core/wisp_engine.c:677-686
+ *   cpu_gemv_t_f16       csrc/core/wisp_engine.c:647-658
+ *   cpu_rmsnorm          csrc/core/wisp_engine.c:660-671
+ *   cpu_residual_add     csrc/core/wisp_engine.c:673-675
  *   cpu_router_topk      csrc/core/wisp_engine.c:782-818
  *   cpu_expert_ffn       csrc/core/wisp_engine.c:1534-1561
  *   wisp_expert_fetch    csrc/core/wisp_engine.c:1138-1296 (tier policy)
@@ -34,6 +37,19 @@ void ref_gemv_f16(const uint16_t* W, const float* x, float* y, int rows,
 
 void ref_swiglu(const float* g, const float* u, float* o, int n) {
     cpu_swiglu(g, u, o, n);
+}
+
+void ref_gemv_t_f16(const uint16_t* W, const float* x, float* y, int rows,
+                    int cols) {
+    cpu_gemv_t_f16((const wisp_half*)W, x, y, rows, cols);
+}
+
+void ref_rmsnorm(const float* x, const uint16_t* w, float* y, int n, float eps) {
+    cpu_rmsnorm(x, (const wisp_half*)w, y, n, eps);
+}
+
+void ref_residual_add(float* x, const float* d, int n) {
+    cpu_residual_add(x, d, n);
 }
 
 void ref_router_topk(const uint16_t* W, const uint16_t* bias, const float* x,

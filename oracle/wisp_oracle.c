@@ -289,6 +289,35 @@ void orc_gemv_f16(const uint16_t* W, const float* x, float* y,
     }
 }
 
+/* y[c] = sum_r fp32(W[r,c]) * x[r], rows in order
+ * (csrc/core/wisp_engine.c:647-658). */
+void orc_gemv_t_f16(const uint16_t* W, const float* x, float* y,
+                    int rows, int cols) {
+    int c;
+    #pragma omp parallel for schedule(static)
+    for (c = 0; c < cols; c++) {
+        float acc = 0.0f;
+        for (int r = 0; r < rows; r++)
+            acc = acc + orc_half_to_float(W[(size_t)r * (size_t)cols + c]) * x[r];
+        y[c] = acc;
+    }
+}
+
+/* y = x * (float)(1 / sqrt(ss / n + eps)) * fp32(w), the sum of squares ss
+ * accumulated in double (csrc/core/wisp_engine.c:660-671, scalar branch);
+ * y may alias x. */
+void orc_rmsnorm(const float* x, const uint16_t* w, float* y, int n, float eps) {
+    double ss = 0.0;
+    for (int i = 0; i < n; i++) ss += (double)x[i] * x[i];
+    float scale = (float)(1.0 / sqrt(ss / n + eps));
+    for (int i = 0; i < n; i++) y[i] = x[i] * scale * orc_half_to_float(w[i]);
+}
+
+/* x += d (csrc/core/wisp_engine.c:673-675). */
+void orc_residual_add(float* x, const float* d, int n) {
+    for (int i = 0; i < n; i++) x[i] = x[i] + d[i];
+}
+
 void orc_swiglu(const float* g, const float* u, float* o, int n) {
     for (int i = 0; i < n; i++) {
         float s = g[i] / (1.0f + expf(-g[i]));

@@ -89,6 +89,14 @@ void orc_gemv_int4_f64(const uint8_t* packed, const uint16_t* scales,
 /* y[r] = sum_c fp32(W[r,c]) * x[c] (csrc/core/wisp_engine.c:630-645). */
 void orc_gemv_f16(const uint16_t* W, const float* x, float* y,
                   int rows, int cols);
+/* y[c] = sum_r fp32(W[r,c]) * x[r] (csrc/core/wisp_engine.c:647-658). */
+void orc_gemv_t_f16(const uint16_t* W, const float* x, float* y,
+                    int rows, int cols);
+/* RMSNorm, double sum of squares (csrc/core/wisp_engine.c:660-671, scalar
+ * branch); y may alias x. */
+void orc_rmsnorm(const float* x, const uint16_t* w, float* y, int n, float eps);
+/* x += d (csrc/core/wisp_engine.c:673-675). */
+void orc_residual_add(float* x, const float* d, int n);
 /* o = g / (1 + expf(-g)) * u (csrc/core/wisp_engine.c:677-686). */
 void orc_swiglu(const float* g, const float* u, float* o, int n);
 /* acc += w * x (csrc/core/wisp_engine.c:688-690). */

@@ -7,6 +7,8 @@ Every expected output here is produced by the REFERENCE's own C code
   gemv_int4.npz       cpu_gemv_int4, scalar branch   (wisp_engine.c:822-845)
   expert_ffn.npz      cpu_expert_ffn                 (wisp_engine.c:1534-1561)
   router_softmax.npz  cpu_router_topk                (wisp_engine.c:782-818)
+  layer_ops.npz       cpu_rmsnorm, cpu_gemv_t_f16,   (wisp_engine.c:647-675)
+                      cpu_residual_add
 The fp16 column of dequant_g64 is the fp32 probe value rounded to nearest
 even, which is what the reference GPU kernel stores
 (csrc/cuda/expert_loader.cu:42).
@@ -77,6 +79,25 @@ def main():
     R.ref_router_topk(O._p(W), O._p(bias), O._p(x), O._p(lg), n_exp, hidden, k, O._p(idx), O._p(w))
     np.savez_compressed(os.path.join(HERE, "router_softmax.npz"), W=W.view(np.uint16),
                         bias=bias.view(np.uint16), x=x, k=k, idx=idx, w=w, probs=lg)
+    # the decode step's neighbouring ops: RMSNorm (eps 1e-6, n 7168),
+    # transposed fp16 GEMV [96, 512], residual add
+    rng2 = np.random.default_rng(20261203)
+    n = 7168
+    x = (rng2.standard_normal(n) * 3.0).astype(np.float32)
+    wn = (1.0 + 0.1 * rng2.standard_normal(n)).astype(np.float16)
+    y = np.empty(n, np.float32)
+    R.ref_rmsnorm(O._p(x), O._p(wn), O._p(y), n, np.float32(1e-6))
+    rows, cols = 96, 512
+    Wt = (rng2.standard_normal((rows, cols)) * 0.05).astype(np.float16)
+    xt = rng2.standard_normal(rows).astype(np.float32)
+    yt = np.empty(cols, np.float32)
+    R.ref_gemv_t_f16(O._p(Wt), O._p(xt), O._p(yt), rows, cols)
+    r0 = rng2.standard_normal(n).astype(np.float32)
+    d = rng2.standard_normal(n).astype(np.float32)
+    r1 = r0.copy()
+    R.ref_residual_add(O._p(r1), O._p(d), n)
+    np.savez_compressed(os.path.join(HERE, "layer_ops.npz"), x=x, w=wn.view(np.uint16), eps=1e-6,
+                        y=y, Wt=Wt.view(np.uint16), xt=xt, yt=yt, r0=r0, d=d, r1=r1)
     print("golden fixtures written to", HERE)
 
 

@@ -440,3 +440,55 @@ def test_oracle_vs_golden_router():
     assert idx.tolist() == g["idx"].tolist()
     assert np.allclose(w, g["w"], rtol=1e-5)
     assert np.allclose(probs, g["probs"], rtol=1e-5, atol=1e-9)
+
+
+# --------------------------------------------------------------------------
+# the decode step's neighbouring ops (RMSNorm, residual, transposed GEMV)
+# --------------------------------------------------------------------------
+
+def test_layer_ops_vs_golden():
+    """Fixture written by the reference's scalar C (tests/golden/make_golden.py)."""
+    g = np.load(synth_golden("layer_ops.npz"))
+    assert np.array_equal(O.rmsnorm(g["x"], g["w"], float(g["eps"])), g["y"])
+    # the reference build contracts a * b + acc into an FMA; the oracle does
+    # not (-ffp-contract=off): same sum order, last-bit differences
+    yt = O.gemv_t_f16(g["Wt"], g["xt"])
+    assert np.max(np.abs(yt - g["yt"])) <= 1e-6 * np.max(np.abs(g["yt"]))
+    assert np.array_equal(O.residual_add(g["r0"], g["d"]), g["r1"])
+
+
+@needs_ref
+def test_layer_ops_match_reference_scalar_c():
+    rng = np.random.default_rng(41)
+    for n in (1, 7, 4096, 7169):
+        x = (rng.standard_normal(n) * 2).astype(np.float32)
+        w = (1 + 0.2 * rng.standard_normal(n)).astype(np.float16)
+        want = np.empty(n, np.float32)
+        REF.ref_rmsnorm(O._p(x), O._p(w), O._p(want), n, np.float32(1e-5))
+        assert np.array_equal(O.rmsnorm(x, w, 1e-5), want)
+    W = (rng.standard_normal((33, 70)) * 0.1).astype(np.float16)
+    xt = rng.standard_normal(33).astype(np.float32)
+    want = np.empty(70, np.float32)
+    REF.ref_gemv_t_f16(O._p(W), O._p(xt), O._p(want), 33, 70)
+    assert np.max(np.abs(O.gemv_t_f16(W, xt) - want)) <= 1e-6 * np.max(np.abs(want))
+
+
+def test_layer_ops_closed_forms():
+    """RMSNorm against float64 (scale applied to x, then the fp16 weight;
+    a wrong mean or a missing eps fails), and W^T x against the transposed
+    product."""
+    rng = np.random.default_rng(42)
+    n = 1000
+    x = rng.standard_normal(n).astype(np.float32)
+    w = (1 + 0.3 * rng.standard_normal(n)).astype(np.float16)
+    eps = 1e-2
+    ref = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2) + eps) * \
+        w.astype(np.float64)
+    got = O.rmsnorm(x, w, eps)
+    assert np.max(np.abs(got - ref)) <= 1e-5 * np.max(np.abs(ref))
+    z = O.rmsnorm(np.zeros(16, np.float32), np.ones(16, np.float16), 1e-6)
+    assert not np.any(z)
+    W = rng.standard_normal((40, 24)).astype(np.float16)
+    xt = rng.standard_normal(40).astype(np.float32)
+    want = W.astype(np.float64).T @ xt.astype(np.float64)
+    assert np.max(np.abs(O.gemv_t_f16(W, xt) - want)) <= 1e-5 * np.max(np.abs(want))

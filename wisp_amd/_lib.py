@@ -36,6 +36,10 @@ _SIGS = {
     "wisp_gpu_swiglu_ffn": (None, [P, P, P, P, c_int, c_int, P]),
     "wisp_gpu_scale_accum": (None, [P, P, c_float, c_int, P]),
     "wisp_gpu_router_topk": (None, [P, P, P, P, c_int, c_int, c_int, P, P, P]),
+    "wisp_gpu_gemv_t_f16": (None, [P, P, P, c_int, c_int, P]),
+    "wisp_gpu_rmsnorm": (None, [P, P, P, c_int, c_float, P]),
+    "wisp_gpu_residual_add": (None, [P, P, c_int, P]),
+    "wisp_gpu_swiglu": (None, [P, P, P, c_int, P]),
     # section 2: layout
     "wisp_expert_layout_from_blob": (c_int, [P, c_size_t, POINTER(WispExpertLayout)]),
     "wisp_expert_layout_check": (c_int, [POINTER(WispExpertLayout)]),
@@ -53,6 +57,11 @@ _SIGS = {
                                                P, c_int, c_int, c_int, c_int, P, c_size_t, c_int,
                                                P, P, P]),
     "wisp_moe_decode_status": (c_int, [P, P, P, c_int]),
+    "wisp_moe_block_workspace_bytes": (c_size_t, [POINTER(WispExpertLayout), c_int, c_int, c_int,
+                                                  c_int]),
+    "wisp_gpu_moe_block_int4": (c_int, [P, P, c_float, P, P, c_int, P, P, P, P, P,
+                                        POINTER(WispExpertLayout), c_int, c_int, c_int, P,
+                                        c_size_t, P]),
     "wisp_gpu_moe_layer_decode_int4_noalloc": (c_int, [P, P, c_int, P, P, P, P, P,
                                                        POINTER(WispExpertLayout), P, c_int, c_int,
                                                        c_int, c_int, c_int, P, P, P]),

@@ -1521,6 +1521,84 @@ extern "C" hipError_t wisp_gpu_moe_layer_decode_int4_noalloc(
                      WISP_NOALLOC_SCRATCH_BYTES, accumulate, d_out_f32, d_out_f16, s);
 }
 
+/* ---- the FFN half of a decode step (RMSNorm, MoE layer, residual) ------- */
+
+/* The fixed leading regions of every decode workspace (unique count and
+ * status, routing epoch, routing words): the block's prefill path starts
+ * after them, so a workspace shared by both paths keeps its routing state. */
+#define DEC_WS_HEADER ((size_t)512 + (size_t)DEC_MAX_TOKENS * DEC_ROUTE_MAX_EXPERTS * 8)
+
+hipError_t wisp_amd__rmsnorm_rows(const float* x, const wisp_half* w, float* y32, wisp_half* y16,
+                                  int rows, int n, float eps, hipStream_t s);
+
+struct BlockWs {
+    size_t pf, xn, total;
+    bool decode;
+};
+
+static BlockWs block_ws(const WispExpertLayout* L, int M, int top_k, int n_experts,
+                        int has_shared) {
+    BlockWs b = {0, 0, 0, M <= DEC_MAX_TOKENS};
+    const size_t hidden = L->cols[0];
+    if (b.decode) {
+        b.xn = align_up(ws_layout(L, M, top_k, has_shared).total, 256);
+        b.total = b.xn + align_up((size_t)M * hidden * 4, 256);
+    } else {
+        b.pf = wisp_moe_prefill_workspace_bytes(L, M, top_k, n_experts, has_shared);
+        if (b.pf == 0) return b;
+        b.xn = align_up(DEC_WS_HEADER + b.pf, 256);
+        b.total = b.xn + align_up((size_t)M * hidden * 2, 256);
+    }
+    return b;
+}
+
+extern "C" size_t wisp_moe_block_workspace_bytes(const WispExpertLayout* L, int n_tokens,
+                                                 int top_k, int n_experts, int has_shared) {
+    if (!L || n_tokens < 1 || top_k < 1 || top_k > DEC_MAX_TOPK || n_experts < 1 ||
+        n_experts > DEC_ROUTE_MAX_EXPERTS || wisp_expert_layout_check(L) != hipSuccess)
+        return 0;
+    return block_ws(L, n_tokens, top_k, n_experts, has_shared).total;
+}
+
+extern "C" hipError_t wisp_gpu_moe_block_int4(
+    float* d_x, const wisp_half* d_post_norm_w, float eps, const wisp_half* d_router_w,
+    const wisp_half* d_router_bias, int router_kind, float* d_scores, int* d_topk_idx,
+    float* d_topk_w, const void* const* d_expert_table, const void* d_shared_blob,
+    const WispExpertLayout* L, int n_tokens, int top_k, int n_experts, void* d_workspace,
+    size_t workspace_bytes, hipStream_t s) {
+    const int M = n_tokens;
+    if (!d_x || !d_post_norm_w || !d_workspace || M < 1 || top_k < 1 || top_k > DEC_MAX_TOPK ||
+        n_experts < 1 || n_experts > DEC_ROUTE_MAX_EXPERTS || !d_expert_table ||
+        !layer_args_ok(d_router_w, router_kind, d_scores, d_topk_idx, d_topk_w, top_k, n_experts,
+                       L))
+        return hipErrorInvalidValue;
+    const BlockWs b = block_ws(L, M, top_k, n_experts, d_shared_blob != nullptr);
+    if (b.total == 0 || workspace_bytes < b.total) return hipErrorInvalidValue;
+    const int hidden = (int)L->cols[0];
+    char* ws = (char*)d_workspace;
+    hipError_t e;
+    if (b.decode) {
+        /* fp32 normalised rows: the router runs in fp32, the experts read
+         * an fp16 copy made by the prep workgroup */
+        float* xn = (float*)(ws + b.xn);
+        e = wisp_amd__rmsnorm_rows(d_x, d_post_norm_w, xn, nullptr, M, hidden, eps, s);
+        if (e != hipSuccess) return e;
+        return layer_run(d_router_w, d_router_bias, router_kind, d_scores, d_topk_idx, d_topk_w,
+                         d_expert_table, d_shared_blob, L, xn, WISP_DTYPE_F32, M, top_k,
+                         n_experts, d_workspace, b.xn, /*accumulate=*/1, d_x, nullptr, s);
+    }
+    if ((uintptr_t)d_x % 16) return hipErrorInvalidValue;   /* the prefill's fp32 output */
+    wisp_half* xn = (wisp_half*)(ws + b.xn);
+    e = wisp_amd__rmsnorm_rows(d_x, d_post_norm_w, nullptr, xn, M, hidden, eps, s);
+    if (e != hipSuccess) return e;
+    e = wisp_gpu_moe_route(d_router_w, d_router_bias, xn, M, hidden, n_experts, top_k,
+                           router_kind, d_scores, d_topk_idx, d_topk_w, s);
+    if (e != hipSuccess) return e;
+    return wisp_gpu_moe_prefill_int4(d_expert_table, d_shared_blob, L, xn, M, d_topk_idx,
+                                     d_topk_w, top_k, n_experts, ws + DEC_WS_HEADER, b.pf,
+                                     /*accumulate=*/1, d_x, nullptr, s);
+}
+
 extern "C" hipError_t wisp_moe_decode_status(void* d_workspace, hipStream_t s, uint32_t* flags,
                                              int clear) {
     if (!flags) return hipErrorInvalidValue;

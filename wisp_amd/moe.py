@@ -153,3 +153,21 @@ def decode_status(ws: DeviceBuffer | None, stream: int = 0, clear: bool = True) 
                                       ctypes.byref(flags), 1 if clear else 0)
     _ck(rc, "wisp_moe_decode_status")
     return int(flags.value)
+
+
+def block_workspace_bytes(layout: WispExpertLayout, n_tokens: int, top_k: int, n_experts: int,
+                          has_shared: bool) -> int:
+    return int(lib().wisp_moe_block_workspace_bytes(ctypes.byref(layout), n_tokens, top_k,
+                                                     n_experts, 1 if has_shared else 0))
+
+
+def moe_block_int4(x: int, post_norm_w: int, eps: float, router_w: int, router_bias: int,
+                   kind: int, scores: int, idx: int, w: int, table: int, shared_blob: int,
+                   layout: WispExpertLayout, n_tokens: int, top_k: int, n_experts: int,
+                   ws: DeviceBuffer, stream: int = 0) -> None:
+    """x += MoE(RMSNorm(x) * post_norm_w) for n_tokens fp32 rows (in place)."""
+    rc = lib().wisp_gpu_moe_block_int4(x, post_norm_w, eps, router_w, router_bias or None, kind,
+                                       scores, idx, w, table, shared_blob or None,
+                                       ctypes.byref(layout), n_tokens, top_k, n_experts, ws.ptr,
+                                       ws.nbytes, stream or None)
+    _ck(rc, "wisp_gpu_moe_block_int4")
