@@ -422,8 +422,12 @@ enum {
  * VRAM_HITS / LOOKUPS; the reference reports (vram + ram) / total
  * (csrc/core/wisp_engine.c:2343-2344), which is always 1 here. */
 enum {
-    WISP_TIER_LOOKUPS = 0, WISP_TIER_VRAM_HITS, WISP_TIER_RAM_HITS, WISP_TIER_FIRST_TOUCH,
+    WISP_TIER_LOOKUPS = 0, WISP_TIER_VRAM_HITS, WISP_TIER_RAM_HITS,
+    WISP_TIER_FIRST_TOUCH,       /* SSD misses: first touches, and experts back after a RAM eviction */
     WISP_TIER_PROMOTIONS, WISP_TIER_EVICTIONS, WISP_TIER_SCRATCH_SERVES, WISP_TIER_H2D_BYTES,
+    WISP_TIER_RAM_EVICTIONS,     /* bounded RAM tier: experts dropped from RAM  */
+    WISP_TIER_SSD_BYTES,         /* bounded RAM tier: bytes read from expert files */
+    WISP_TIER_D2H_BYTES,         /* bounded RAM tier: evicted experts copied back */
     WISP_TIER_N_STATS
 };
 
@@ -433,6 +437,14 @@ typedef struct WispTierPolicy WispTierPolicy;
 WispTierPolicy* wisp_tier_policy_create(int n_layers, int n_experts,
                                         int n_slots, int scratch_slots,
                                         int promote_hits);
+/* The same policy with a RAM tier of n_ram_slots blobs over the expert
+ * files (the reference's RAM LRU with its byte budget, :1053-1068; an
+ * expert dropped from RAM loses its hit count and comes back as an SSD
+ * miss; a VRAM victim is copied back into RAM). n_ram_slots must exceed
+ * scratch_slots. */
+WispTierPolicy* wisp_tier_policy_create_ram(int n_layers, int n_experts,
+                                            int n_ram_slots, int n_slots,
+                                            int scratch_slots, int promote_hits);
 void wisp_tier_policy_destroy(WispTierPolicy* t);
 /* Starts the lookups of one layer: experts resolved from here on are not
  * evicted until the next call. */
@@ -458,6 +470,22 @@ WispExpertTier* wisp_tier_create(int n_layers, int n_experts,
                                  const void* const* host_blobs, int n_slots,
                                  int scratch_slots, int promote_hits,
                                  hipError_t* err);
+/* The three-tier cache: VRAM slots, a RAM tier of n_ram_slots pinned blob
+ * slots (> scratch_slots), and the expert files under model_path
+ * (<model_path>/experts/L%03u_E%05u.bin, each blob_bytes long) as the SSD
+ * tier. An SSD miss reads its file into a RAM slot (the LRU RAM entry is
+ * dropped when the tier is full; experts of the layer being fetched are
+ * kept), in parallel threads for the misses of one layer, then copies as
+ * a RAM hit would; a VRAM victim of a promotion is copied back into RAM
+ * (device to host on the tier's stream). Replaces the SSD path of
+ * wisp_expert_fetch (csrc/core/wisp_engine.c:1205-1296) and its pinned
+ * staging pool (csrc/core/mem_pool.c:27-122). A missing or short file
+ * makes wisp_tier_fetch_layer return hipErrorFileNotFound. */
+WispExpertTier* wisp_tier_create_ssd(int n_layers, int n_experts,
+                                     size_t blob_bytes, const char* model_path,
+                                     int n_ram_slots, int n_slots,
+                                     int scratch_slots, int promote_hits,
+                                     hipError_t* err);
 void wisp_tier_destroy(WispExpertTier* t);
 /* Device table row of a layer: [n_experts] blob pointers, valid for the
  * experts of the last wisp_tier_fetch_layer of that layer. */

@@ -6,6 +6,8 @@ holding the right blob when it is read.
 
 Bar: the fp16 parity bar of tests/gpu_util.py per token and layer; copy
 accounting exact (every lookup that is not a VRAM hit copies one blob)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -76,6 +78,83 @@ def test_streaming_layers_match_oracle(zeros, shared):
     assert s["lookups"] == s["vram_hits"] + s["ram_hits"] + s["first_touch"]
     assert s["h2d_bytes"] == not_hits * size
     assert s["promotions"] > 0 and s["evictions"] > 0 and s["vram_hits"] > 0, s
+    t.close()
+    synchronize()
+
+
+@pytest.mark.parametrize("zeros", [False, True])
+def test_ssd_tier_streaming_matches_oracle(tmp_path, zeros):
+    """Three tiers: expert files on disk (the SSD tier), a RAM tier of 14
+    pinned slots, 5 VRAM slots; the routing makes experts drop out of RAM,
+    come back from their files, get promoted and evicted (copied back to
+    RAM). Every token and layer against the oracle; the executor's paths
+    against the policy alone on the same ids; exact byte accounting."""
+    print(f"ssd tier zeros={zeros}", flush=True)
+    L, E, inter, hidden, gs, M, k, steps, slots, n_ram = 3, 12, 256, 512, 128, 2, 3, 16, 5, 14
+    rng = np.random.default_rng(40 + zeros)
+    os.makedirs(tmp_path / "experts")
+    blobs = {}
+    for l in range(L):
+        for e in range(E):
+            b = make_expert(seed=500 + 1000 * l, e=e, inter=inter, hidden=hidden, gs=gs,
+                            zeros=zeros)
+            blobs[(l, e)] = b
+            b.tofile(tmp_path / "experts" / f"L{l:03d}_E{e:05d}.bin")
+    size = synth.blob_size(inter, hidden, gs)
+    layout = moe.layout_from_blob(blobs[(0, 0)], has_zeros=zeros)
+    t = tier.ExpertTier(L, E, size, None, slots, scratch_slots=M * k + 2,
+                        model_path=str(tmp_path), n_ram_slots=n_ram)
+    pol = tier.Policy(L, E, slots, M * k + 2, n_ram_slots=n_ram)
+    st = Stream()
+    ws = DeviceBuffer(moe.decode_workspace_bytes(layout, M, k, False))
+    out32 = DeviceBuffer(4 * M * hidden)
+    for step in range(steps):
+        for l in range(L):
+            idx = synth.zipf_topk(rng, M, E, k, s=1.1)
+            w = synth.route_weights(rng, M, k)
+            x = synth.make_x(rng, M, hidden)
+            dx = to_device(x)
+            uniq = list(dict.fromkeys(int(e) for e in idx.reshape(-1)))
+            pol.begin_layer()
+            want_paths = [pol.lookup(l, e)[0] for e in uniq]
+            paths = t.fetch_layer(l, uniq, st.handle)
+            assert paths.tolist() == want_paths, (step, l)
+            t.wait_copies(st.handle)
+            di, dw = to_device(idx), to_device(w)
+            moe.moe_decode_int4(t.table(l), 0, layout, dx.ptr, M, di.ptr, dw.ptr, k, E, ws,
+                                out32=out32.ptr, stream=st.handle)
+            t.release_layer(st.handle)
+            st.synchronize()
+            g32 = out32.download(np.float32, (M, hidden))
+            lb = [blobs[(l, e)] for e in range(E)]
+            for v in range(M):
+                want = O.moe_combine(lb, None, x[v].astype(np.float32), idx[v], w[v])
+                assert_close(g32[v], want, f"step {step} layer {l} token {v}")
+    s = t.stats()
+    ps = pol.stats()
+    for key in ("lookups", "vram_hits", "ram_hits", "first_touch", "promotions", "evictions",
+                "ram_evictions"):
+        assert s[key] == ps[key], key
+    assert s["ssd_bytes"] == s["first_touch"] * size
+    assert s["h2d_bytes"] == (s["lookups"] - s["vram_hits"]) * size
+    assert s["ram_evictions"] > 0 and s["promotions"] > 0 and s["evictions"] > 0, s
+    assert s["first_touch"] > len(blobs) // 2
+    assert s["d2h_bytes"] > 0 and s["d2h_bytes"] % size == 0   # VRAM victims copied back
+    print(f"  stats {s}", flush=True)
+    t.close()
+    synchronize()
+
+
+def test_ssd_tier_missing_file_is_an_error(tmp_path):
+    os.makedirs(tmp_path / "experts")
+    inter, hidden, gs = 256, 512, 128
+    b = make_expert(3, 0, inter, hidden, gs)
+    b.tofile(tmp_path / "experts" / "L000_E00000.bin")
+    t = tier.ExpertTier(1, 4, b.nbytes, None, 2, scratch_slots=3, model_path=str(tmp_path),
+                        n_ram_slots=4)
+    assert t.fetch_layer(0, [0]).tolist() == [tier.COLD_VRAM]
+    with pytest.raises(Exception, match="wisp_tier_fetch_layer"):
+        t.fetch_layer(0, [1])
     t.close()
     synchronize()
 

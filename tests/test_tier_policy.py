@@ -60,6 +60,75 @@ def test_paths_match_reference(tmp_path, n_slots, seed):
         assert all(seen[p] > 0 for p in range(5)), seen
 
 
+@needs_ref
+@pytest.mark.parametrize("n_slots,n_ram,seed", [(6, 12, 5), (10, 8, 6), (4, 24, 7), (0, 10, 8),
+                                                (12, 30, 9)])
+def test_paths_match_reference_with_bounded_ram(tmp_path, n_slots, n_ram, seed):
+    """The three-tier case: the reference's RAM LRU with a byte budget of
+    n_ram blobs (entries dropped when full, hit counts lost, VRAM victims
+    copied back) against the policy's bounded RAM tier, path by path."""
+    L, E, k, steps = 3, 16, 4, 60
+    inter, hidden, gs = 128, 128, 128
+    os.makedirs(tmp_path / "experts")
+    size = None
+    for l in range(L):
+        for e in range(E):
+            b = synth.make_blob(np.random.default_rng([l, e]), inter, hidden, gs, layer=l, expert=e)
+            size = b.nbytes
+            b.tofile(tmp_path / "experts" / f"L{l:03d}_E{e:05d}.bin")
+    scratch = min(k + 2, 16)
+    ref = REF.ref_tier_create(str(tmp_path).encode(), L, k, size, n_slots * size, n_ram * size)
+    pol = tier.Policy(L, E, n_slots, scratch, n_ram_slots=n_ram)
+    trace = zipf_trace(np.random.default_rng(seed), steps, L, E, k)
+    seen = {p: 0 for p in range(5)}
+    for t, layers in enumerate(trace):
+        for l, ids in enumerate(layers):
+            pol.begin_layer()
+            for e in ids:
+                want = REF.ref_tier_fetch(ref, l, int(e))
+                got, _, _ = pol.lookup(l, int(e))
+                assert got == want, (t, l, int(e), got, want)
+                seen[got] += 1
+    counts = np.zeros(5, np.uint64)
+    REF.ref_tier_stats(ref, counts.ctypes.data)
+    st = pol.stats()
+    assert (st["vram_hits"], st["ram_hits"], st["first_touch"]) == tuple(int(c) for c in counts[:3])
+    if n_ram < L * E:
+        assert st["ram_evictions"] > 0
+        # more SSD reads than distinct experts: some came back after a RAM eviction
+        distinct = len({(l, int(e)) for layers in trace for l, ids in enumerate(layers) for e in ids})
+        assert st["first_touch"] > distinct
+
+
+def test_bounded_ram_drops_hit_counts():
+    """An expert dropped from the RAM tier loses its hit count: it comes
+    back as an SSD miss and needs three more RAM hits to be promoted."""
+    p = tier.Policy(1, 8, 1, 2, n_ram_slots=3)
+    order = [0, 0, 1, 2, 3, 0, 0, 0, 0]
+    paths = []
+    for e in order:
+        p.begin_layer()
+        paths.append(p.lookup(0, e)[0])
+    # 0 takes the one VRAM slot; 1, 2, 3 are SSD misses through scratch, and
+    # 3 drops the LRU RAM entry (0, which sits in VRAM); 0 is still a VRAM hit
+    assert paths[:5] == [tier.COLD_VRAM, tier.VRAM_HIT, tier.COLD_SCRATCH, tier.COLD_SCRATCH,
+                         tier.COLD_SCRATCH]
+    assert paths[5:] == [tier.VRAM_HIT] * 4
+    st = p.stats()
+    assert st["ram_evictions"] == 1 and st["first_touch"] == 4
+    q = tier.Policy(1, 8, 0, 2, n_ram_slots=3)
+    paths = []
+    for e in [5, 5, 6, 7, 4, 5, 5, 5]:
+        q.begin_layer()
+        paths.append(q.lookup(0, e)[0])
+    # 5 earns one RAM hit, is dropped by 4 (LRU after 6, 7 came in), then is an
+    # SSD miss again with a fresh count: two RAM hits later it still rides scratch
+    assert paths == [tier.COLD_SCRATCH, tier.RAM_SCRATCH, tier.COLD_SCRATCH, tier.COLD_SCRATCH,
+                     tier.COLD_SCRATCH, tier.COLD_SCRATCH, tier.RAM_SCRATCH, tier.RAM_SCRATCH]
+    with pytest.raises(ValueError):
+        tier.Policy(1, 8, 0, 4, n_ram_slots=4)       # must exceed the scratch ring
+
+
 def test_promotion_on_third_ram_hit_and_lru_eviction():
     # 1 layer, 4 experts, 2 slots, scratch ring of 3. A first touch sets the
     # RAM hit count to 0 (the reference's SSD-miss path); promotion comes on

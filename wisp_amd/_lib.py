@@ -72,11 +72,14 @@ _SIGS = {
                                           c_int, P, c_size_t, c_int, P, P, P]),
     # section 6: VRAM tier
     "wisp_tier_policy_create": (c_void_p, [c_int, c_int, c_int, c_int, c_int]),
+    "wisp_tier_policy_create_ram": (c_void_p, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "wisp_tier_policy_destroy": (None, [P]),
     "wisp_tier_policy_begin_layer": (None, [P]),
     "wisp_tier_policy_lookup": (c_int, [P, c_int, c_int, P, P, P]),
     "wisp_tier_policy_stats": (None, [P, P]),
     "wisp_tier_create": (c_void_p, [c_int, c_int, c_size_t, P, c_int, c_int, c_int, P]),
+    "wisp_tier_create_ssd": (c_void_p, [c_int, c_int, c_size_t, c_char_p, c_int, c_int, c_int,
+                                        c_int, P]),
     "wisp_tier_destroy": (None, [P]),
     "wisp_tier_device_table": (c_void_p, [P, c_int]),
     "wisp_tier_fetch_layer": (c_int, [P, c_int, P, c_int, P, P]),

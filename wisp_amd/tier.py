@@ -4,6 +4,7 @@ C-ABI."""
 from __future__ import annotations
 
 import ctypes
+import os
 
 import numpy as np
 
@@ -12,7 +13,7 @@ from .hip import check
 
 VRAM_HIT, RAM_SCRATCH, RAM_PROMOTE, COLD_VRAM, COLD_SCRATCH = 0, 1, 2, 3, 4
 STAT_NAMES = ("lookups", "vram_hits", "ram_hits", "first_touch", "promotions", "evictions",
-              "scratch_serves", "h2d_bytes")
+              "scratch_serves", "h2d_bytes", "ram_evictions", "ssd_bytes", "d2h_bytes")
 PROMOTE_HITS = 3   # the reference's WISP_PROMOTE_HITS
 
 
@@ -20,9 +21,15 @@ class Policy:
     """The tier policy alone (host only, no device calls)."""
 
     def __init__(self, n_layers: int, n_experts: int, n_slots: int, scratch_slots: int,
-                 promote_hits: int = PROMOTE_HITS):
-        self._h = lib().wisp_tier_policy_create(n_layers, n_experts, n_slots, scratch_slots,
-                                                promote_hits)
+                 promote_hits: int = PROMOTE_HITS, n_ram_slots: int | None = None):
+        """n_ram_slots None: every expert sits in RAM; else a RAM tier of
+        that many blobs over the expert files (SSD tier)."""
+        if n_ram_slots is None:
+            self._h = lib().wisp_tier_policy_create(n_layers, n_experts, n_slots, scratch_slots,
+                                                    promote_hits)
+        else:
+            self._h = lib().wisp_tier_policy_create_ram(n_layers, n_experts, n_ram_slots,
+                                                        n_slots, scratch_slots, promote_hits)
         if not self._h:
             raise ValueError("wisp_tier_policy_create rejected its arguments")
 
@@ -56,12 +63,21 @@ class ExpertTier:
     pinned host addresses, layer-major)."""
 
     def __init__(self, n_layers: int, n_experts: int, blob_bytes: int, host_ptrs,
-                 n_slots: int, scratch_slots: int, promote_hits: int = PROMOTE_HITS):
+                 n_slots: int, scratch_slots: int, promote_hits: int = PROMOTE_HITS,
+                 model_path: str | None = None, n_ram_slots: int = 0):
+        """host_ptrs: pinned blobs of every expert (RAM tier holds all), or
+        None with model_path and n_ram_slots: a bounded RAM tier over the
+        expert files (wisp_tier_create_ssd)."""
         self.n_layers, self.n_experts = n_layers, n_experts
-        self._ptrs = (ctypes.c_void_p * (n_layers * n_experts))(*host_ptrs)
         err = ctypes.c_int(0)
-        self._h = lib().wisp_tier_create(n_layers, n_experts, blob_bytes, self._ptrs, n_slots,
-                                         scratch_slots, promote_hits, ctypes.byref(err))
+        if host_ptrs is not None:
+            self._ptrs = (ctypes.c_void_p * (n_layers * n_experts))(*host_ptrs)
+            self._h = lib().wisp_tier_create(n_layers, n_experts, blob_bytes, self._ptrs, n_slots,
+                                             scratch_slots, promote_hits, ctypes.byref(err))
+        else:
+            self._h = lib().wisp_tier_create_ssd(n_layers, n_experts, blob_bytes,
+                                                 os.fsencode(model_path), n_ram_slots, n_slots,
+                                                 scratch_slots, promote_hits, ctypes.byref(err))
         if not self._h:
             check(err.value or 1, "wisp_tier_create")
 
