@@ -562,7 +562,9 @@ struct Stage16 {
         }
     }
     /* perm: permute each piece (8 fp16) into unpack8_magic slot order with
-     * odd elements divided by 16 (exact: a power-of-two scale). */
+     * odd elements divided by 16 (a power-of-two scale: exact for
+     * |x| >= 2^-10; below that x / 16 is an fp16 subnormal and keeps fewer
+     * bits, an error below 2^-24 absolute). */
     template <bool PERM>
     __device__ __forceinline__ void commit(uint8_t* dst, int dst_stride) const {
         const int total = rows * w16;
@@ -648,8 +650,8 @@ __device__ __forceinline__ void compute_blocks(const u4 (&w)[NB][NT], const uint
 
 /* Copies the first `len` elements of M activation rows (fp16, row stride
  * K) into the LDS x image, permuting each 8-element block into
- * unpack8_magic slot order with odd elements divided by 16 (exact: a
- * power-of-two scale). 16-byte accesses. */
+ * unpack8_magic slot order with odd elements divided by 16 (exact for
+ * |x| >= 2^-10, see Stage16::commit). 16-byte accesses. */
 template <int M>
 __device__ __forceinline__ void stage_x_perm(uint8_t* smem, const LdsMap& L,
                                              const uint16_t* __restrict__ src, int K, int len) {
