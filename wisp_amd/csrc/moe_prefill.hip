@@ -46,6 +46,7 @@
 #define PF_SCALE_LDS_MAX 40960    /* byte budget of the LDS scale (and zero) image */
 #define PF_SCALE_LDS_WIDE 65536   /* the same for the wide full-tile kernel      */
 #define PF_SCALE_PIECES 4         /* 16-byte scale pieces per lane and row tile when staged */
+#define PF_CHUNK 8                /* K blocks per straight-line pipeline chunk (when they divide K) */
 
 struct PfParams {
     uint64_t p_off[3], s_off[3], z_off[3];
@@ -232,7 +233,7 @@ __device__ __forceinline__ h8 dequant8(uint32_t w, h2 s2, h2 z2, uint32_t m, uin
  * them from there. Otherwise every step loads one 2-byte scale per lane and
  * row tile, 16 rows and so 16 memory transactions per instruction: 18 % of
  * the DeepSeek-V3 prefill layer on MI355X. */
-template <bool GATEUP, bool HZ, int TV, int R, int WV, bool SS, int NT>
+template <bool GATEUP, bool HZ, int TV, int R, int WV, bool SS, int NT, int CH = 0>
 __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int cls) {
     constexpr int THREADS = 64 * WV;
     constexpr int FEAT = 8 * NT * WV;            /* gate/up: h features per workgroup */
@@ -337,27 +338,39 @@ __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int 
 
     __syncthreads();   /* s_row visible */
 
-    /* A staging: BM rows x 128 K of a block, 16 B pieces */
+    /* A staging: BM rows x 128 K of a block, 16 B pieces. In the chunked
+     * loop (CH > 0) every load is unconditional: a padding row reads the
+     * tile's first row and is zeroed when committed, so no load sits under
+     * an exec mask (whose zero default the compiler keeps in a copied
+     * register, and every copy of an in-flight register is a wait). */
     const uint16_t* asrc = GATEUP ? P.x : P.H;
     u4 areg[APT];
     int aoff[APT];     /* element offset of each piece's source row (-1: zero) */
+    bool alive[APT];
 #pragma unroll
     for (int c = 0; c < APT; c++) {
         const int i = threadIdx.x + c * THREADS;
         const int src = s_row[i >> 4];
-        aoff[c] = src >= 0 ? src * K + 8 * (i & 15) : -1;
+        alive[c] = src >= 0;
+        if (CH > 0) aoff[c] = (src >= 0 ? src : s_row[0]) * K + 8 * (i & 15);
+        else aoff[c] = src >= 0 ? src * K + 8 * (i & 15) : -1;
     }
     auto a_issue = [&](int b) {
 #pragma unroll
-        for (int c = 0; c < APT; c++)
-            areg[c] = aoff[c] >= 0 ? *(const u4*)(asrc + (size_t)aoff[c] + b * 128)
-                                   : (u4){0u, 0u, 0u, 0u};
+        for (int c = 0; c < APT; c++) {
+            if (CH > 0) areg[c] = *(const u4*)(asrc + (size_t)aoff[c] + b * 128);
+            else
+                areg[c] = aoff[c] >= 0 ? *(const u4*)(asrc + (size_t)aoff[c] + b * 128)
+                                       : (u4){0u, 0u, 0u, 0u};
+        }
     };
     auto a_commit = [&](int buf) {
 #pragma unroll
         for (int c = 0; c < APT; c++) {
             const int i = threadIdx.x + c * THREADS;
-            *(u4*)(&s_a[buf][(i >> 4) * PF_AROW + 8 * (i & 15)]) = perm8_halves(areg[c]);
+            u4 v = perm8_halves(areg[c]);
+            if (CH > 0 && !alive[c]) v = (u4){0u, 0u, 0u, 0u};
+            *(u4*)(&s_a[buf][(i >> 4) * PF_AROW + 8 * (i & 15)]) = v;
         }
     };
 
@@ -384,70 +397,148 @@ __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int 
     asm volatile("" : "+v"(nib_mask));
     asm volatile("" : "+v"(nib_one));
 
-    a_issue(0);
-    a_commit(0);
-    if (nblk > 1) a_issue(1);
+    /* computes block b from ring slot r and the A buffer of b */
+    auto compute_block = [&](int b, int r) {
+        const uint16_t* abuf = &s_a[b & 1][0];
+        if (SS) {
+            const int g = (b * 128 + 32 * j) >> gshift;
 #pragma unroll
-    for (int r = 0; r < R - 1; r++) w_issue(r, r);
-    __syncthreads();
+            for (int s = 0; s < NT; s++) {
+                sr[r][s] = s_sc[(s * 16 + col) * G + g];
+                if (HZ) zr[r][s] = s_zc[(s * 16 + col) * G + g];
+            }
+        }
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            if constexpr (NT > 2) {
+                /* wide waves: the NT weight fragments first, then one
+                 * activation fragment at a time (registers) */
+                h8 bf[NT];
+#pragma unroll
+                for (int s = 0; s < NT; s++) {
+                    const f16 sc = __builtin_bit_cast(f16, sr[r][s]);
+                    const f16 zc = HZ ? __builtin_bit_cast(f16, zr[r][s]) : (f16)0.0f;
+                    bf[s] = dequant8<HZ>(wr[r][s][kk], (h2){sc, sc}, (h2){zc, zc},
+                                         nib_mask, nib_one);
+                }
+#pragma unroll
+                for (int t = 0; t < TV; t++) {
+                    const h8 af =
+                        *(const h8*)(abuf + (16 * t + col) * PF_AROW + 32 * j + 8 * kk);
+#pragma unroll
+                    for (int s = 0; s < NT; s++)
+                        acc[t][s] = mfma16x16x32(af, bf[s], acc[t][s]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            } else {
+                h8 af[TV];
+#pragma unroll
+                for (int t = 0; t < TV; t++)
+                    af[t] = *(const h8*)(abuf + (16 * t + col) * PF_AROW + 32 * j + 8 * kk);
+#pragma unroll
+                for (int s = 0; s < NT; s++) {
+                    const f16 sc = __builtin_bit_cast(f16, sr[r][s]);
+                    const f16 zc = HZ ? __builtin_bit_cast(f16, zr[r][s]) : (f16)0.0f;
+                    const h8 bf = dequant8<HZ>(wr[r][s][kk], (h2){sc, sc}, (h2){zc, zc},
+                                               nib_mask, nib_one);
+#pragma unroll
+                    for (int t = 0; t < TV; t++)
+                        acc[t][s] = mfma16x16x32(af[t], bf, acc[t][s]);
+                }
+            }
+        }
+    };
 
-    for (int b0 = 0; b0 < nblk; b0 += R) {
+    if (CH > 0) {
+        /* K in chunks of CH blocks (nblk % CH == 0, checked by the
+         * launcher), each chunk one straight-line pipeline: A of block b + 2
+         * and the weights of block b + R - 1 are issued during block b, but
+         * nothing in flight crosses the loop's back edge, so the compiler
+         * waits for exactly the loads each step needs instead of draining
+         * the ring; the pipeline refills once per chunk. */
+        for (int c0 = 0; c0 < nblk; c0 += CH) {
+            a_issue(c0);
+            a_commit(c0 & 1);
+            if (CH > 1) a_issue(c0 + 1);
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int b = b0 + r;
-            if (b < nblk) {
-                if (b + 1 < nblk) a_commit((b + 1) & 1);
-                if (b + 2 < nblk) a_issue(b + 2);
-                w_issue((r + R - 1) % R, b + R - 1);
-                const uint16_t* abuf = &s_a[b & 1][0];
-                if (SS) {
-                    const int g = (b * 128 + 32 * j) >> gshift;
+            for (int r = 0; r < R - 1; r++) w_issue(r, c0 + r);
+            __syncthreads();
 #pragma unroll
-                    for (int s = 0; s < NT; s++) {
-                        sr[r][s] = s_sc[(s * 16 + col) * G + g];
-                        if (HZ) zr[r][s] = s_zc[(s * 16 + col) * G + g];
-                    }
-                }
-#pragma unroll
-                for (int kk = 0; kk < 4; kk++) {
-                    if constexpr (NT > 2) {
-                        /* wide waves: the NT weight fragments first, then one
-                         * activation fragment at a time (registers) */
-                        h8 bf[NT];
-#pragma unroll
-                        for (int s = 0; s < NT; s++) {
-                            const f16 sc = __builtin_bit_cast(f16, sr[r][s]);
-                            const f16 zc = HZ ? __builtin_bit_cast(f16, zr[r][s]) : (f16)0.0f;
-                            bf[s] = dequant8<HZ>(wr[r][s][kk], (h2){sc, sc}, (h2){zc, zc},
-                                                 nib_mask, nib_one);
-                        }
-#pragma unroll
-                        for (int t = 0; t < TV; t++) {
-                            const h8 af =
-                                *(const h8*)(abuf + (16 * t + col) * PF_AROW + 32 * j + 8 * kk);
-#pragma unroll
-                            for (int s = 0; s < NT; s++)
-                                acc[t][s] = mfma16x16x32(af, bf[s], acc[t][s]);
-                        }
-                        __builtin_amdgcn_sched_barrier(0);
-                    } else {
-                        h8 af[TV];
-#pragma unroll
-                        for (int t = 0; t < TV; t++)
-                            af[t] = *(const h8*)(abuf + (16 * t + col) * PF_AROW + 32 * j + 8 * kk);
-#pragma unroll
-                        for (int s = 0; s < NT; s++) {
-                            const f16 sc = __builtin_bit_cast(f16, sr[r][s]);
-                            const f16 zc = HZ ? __builtin_bit_cast(f16, zr[r][s]) : (f16)0.0f;
-                            const h8 bf = dequant8<HZ>(wr[r][s][kk], (h2){sc, sc}, (h2){zc, zc},
-                                                       nib_mask, nib_one);
-#pragma unroll
-                            for (int t = 0; t < TV; t++)
-                                acc[t][s] = mfma16x16x32(af[t], bf, acc[t][s]);
-                        }
-                    }
-                }
+            for (int r = 0; r < CH; r++) {
+                const int b = c0 + r;
+                if (r + 1 < CH) a_commit((b + 1) & 1);
+                if (r + 2 < CH) a_issue(b + 2);
+                if (r + R - 1 < CH) w_issue((r + R - 1) % R, b + R - 1);
+                compute_block(b, r % R);
                 __syncthreads();
+            }
+        }
+    } else {
+        a_issue(0);
+        a_commit(0);
+        if (nblk > 1) a_issue(1);
+    #pragma unroll
+        for (int r = 0; r < R - 1; r++) w_issue(r, r);
+        __syncthreads();
+
+        for (int b0 = 0; b0 < nblk; b0 += R) {
+    #pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int b = b0 + r;
+                if (b < nblk) {
+                    if (b + 1 < nblk) a_commit((b + 1) & 1);
+                    if (b + 2 < nblk) a_issue(b + 2);
+                    w_issue((r + R - 1) % R, b + R - 1);
+                    const uint16_t* abuf = &s_a[b & 1][0];
+                    if (SS) {
+                        const int g = (b * 128 + 32 * j) >> gshift;
+    #pragma unroll
+                        for (int s = 0; s < NT; s++) {
+                            sr[r][s] = s_sc[(s * 16 + col) * G + g];
+                            if (HZ) zr[r][s] = s_zc[(s * 16 + col) * G + g];
+                        }
+                    }
+    #pragma unroll
+                    for (int kk = 0; kk < 4; kk++) {
+                        if constexpr (NT > 2) {
+                            /* wide waves: the NT weight fragments first, then one
+                             * activation fragment at a time (registers) */
+                            h8 bf[NT];
+    #pragma unroll
+                            for (int s = 0; s < NT; s++) {
+                                const f16 sc = __builtin_bit_cast(f16, sr[r][s]);
+                                const f16 zc = HZ ? __builtin_bit_cast(f16, zr[r][s]) : (f16)0.0f;
+                                bf[s] = dequant8<HZ>(wr[r][s][kk], (h2){sc, sc}, (h2){zc, zc},
+                                                     nib_mask, nib_one);
+                            }
+    #pragma unroll
+                            for (int t = 0; t < TV; t++) {
+                                const h8 af =
+                                    *(const h8*)(abuf + (16 * t + col) * PF_AROW + 32 * j + 8 * kk);
+    #pragma unroll
+                                for (int s = 0; s < NT; s++)
+                                    acc[t][s] = mfma16x16x32(af, bf[s], acc[t][s]);
+                            }
+                            __builtin_amdgcn_sched_barrier(0);
+                        } else {
+                            h8 af[TV];
+    #pragma unroll
+                            for (int t = 0; t < TV; t++)
+                                af[t] = *(const h8*)(abuf + (16 * t + col) * PF_AROW + 32 * j + 8 * kk);
+    #pragma unroll
+                            for (int s = 0; s < NT; s++) {
+                                const f16 sc = __builtin_bit_cast(f16, sr[r][s]);
+                                const f16 zc = HZ ? __builtin_bit_cast(f16, zr[r][s]) : (f16)0.0f;
+                                const h8 bf = dequant8<HZ>(wr[r][s][kk], (h2){sc, sc}, (h2){zc, zc},
+                                                           nib_mask, nib_one);
+    #pragma unroll
+                                for (int t = 0; t < TV; t++)
+                                    acc[t][s] = mfma16x16x32(af[t], bf, acc[t][s]);
+                            }
+                        }
+                    }
+                    __syncthreads();
+                }
             }
         }
     }
@@ -574,7 +665,8 @@ static void pf_launch_one(const PfParams& P, int gx, int cls, size_t budget, hip
     const size_t lds = (size_t)WV * NT * 16 * G * 2 * (HZ ? 2 : 1);
     const int ny = GATEUP ? P.inter / (8 * NT * WV) : P.hidden / (16 * NT * WV);
     if (lds <= budget && 2 * G <= 64 * PF_SCALE_PIECES) {
-        auto k = pf_gemm_kernel<GATEUP, HZ, TV, R, WV, true, NT>;
+        auto k = (K / 128) % PF_CHUNK == 0 ? pf_gemm_kernel<GATEUP, HZ, TV, R, WV, true, NT, PF_CHUNK>
+                                          : pf_gemm_kernel<GATEUP, HZ, TV, R, WV, true, NT>;
         if (lds > 65536)
             (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
                                       (int)lds);
@@ -602,7 +694,9 @@ static bool pf_launch_wide(const PfParams& P, int gx, hipStream_t s) {
         if (P.inter % (8 * NTW * PF_WAVES) || P.hidden % (16 * NTW * PF_WAVES) ||
             lds > PF_SCALE_LDS_WIDE || 2 * G > 64 * PF_SCALE_PIECES)
             return false;
-        auto k = pf_gemm_kernel<GATEUP, false, 8, 3, PF_WAVES, true, NTW>;
+        auto k = (K / 128) % PF_CHUNK == 0
+                     ? pf_gemm_kernel<GATEUP, false, 8, 3, PF_WAVES, true, NTW, PF_CHUNK>
+                     : pf_gemm_kernel<GATEUP, false, 8, 3, PF_WAVES, true, NTW>;
         if (lds > 65536)
             (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
                                       (int)lds);
