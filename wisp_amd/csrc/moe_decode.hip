@@ -82,6 +82,7 @@ struct DecodeParams {
     int* tile_cnt;        /* [hidden / 16] down workgroups arrived per row tile */
     int* hcnt;            /* [max_u * upe] gate/up workgroups done per wave unit (fused launch) */
     int gsplit;           /* workgroups sharing the K range of one gate/up row tile */
+    int gfinish;          /* separate gate/up launch: K splits added by gateup_finish_kernel */
     int* gcnt;            /* [max_u * inter / 16] split workgroups arrived per gate/up row tile */
     float* gpart;         /* [max_u * inter / 16][gsplit][2][16][M] gate/up K-split partials */
     float* out32;         /* [M][hidden] layer output (either may be null) */
@@ -173,8 +174,8 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     DecodeParams P, RouteArgs R, const void* const* __restrict__ table, const void* shared_blob,
     const XT* __restrict__ x, int top_k, int n_experts) {
     constexpr int NWV = DEC_PREP_THREADS / 64;
-    __shared__ int s_e[DEC_MAX_TOKENS * DEC_MAX_TOPK];
-    __shared__ float s_w[DEC_MAX_TOKENS * DEC_MAX_TOPK];
+    __shared__ __attribute__((aligned(16))) int s_e[DEC_MAX_TOKENS * DEC_MAX_TOPK];
+    __shared__ __attribute__((aligned(16))) float s_w[DEC_MAX_TOKENS * DEC_MAX_TOPK];
     __shared__ int s_wcount[NWV];
     __shared__ const uint8_t* s_tab[DEC_ROUTE_MAX_EXPERTS];
     __shared__ float s_red[32];
@@ -268,7 +269,7 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     for (int e = threadIdx.x; e < n_experts; e += blockDim.x) s_tab[e] = (const uint8_t*)table[e];
     for (int i = threadIdx.x; i < P.hidden / 16; i += blockDim.x) P.tile_cnt[i] = 0;
     for (int i = threadIdx.x; i < P.max_u * P.upe; i += blockDim.x) P.hcnt[i * DEC_HCNT_STRIDE] = 0;
-    if (P.gsplit > 1)
+    if (P.gsplit > 1 && !P.gfinish)   /* arrival counters of the K splits */
         for (int i = threadIdx.x; i < P.max_u * (P.inter / 16); i += blockDim.x) P.gcnt[i] = 0;
     /* x -> fp16 copy when the gate/up kernel cannot read the caller's x */
     if (P.xconv) {
@@ -407,12 +408,34 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
         e = s_e[p];
         if (e < 0 || e >= n_experts) e = -1;
     }
-    int first_p = -1;
-    if (e >= 0) {
-        for (int q = 0; q < p; q++)
-            if (s_e[q] == e) { first_p = q; break; }
+    /* Every pair against every pair, lane-parallel: the pair list is read
+     * 4 entries at a time with every lane reading the same 16 bytes (a
+     * broadcast), unrolled so the reads are in flight together; a loop of
+     * dependent single reads costs an LDS round trip per pair. A pair is
+     * its expert's first when no earlier pair names the same expert; the
+     * first one also sums every token's weight for the expert, in flat
+     * pair order. Waves past the pairs skip the scan (the trip count is
+     * uniform within a wave). */
+    bool is_first = e >= 0;
+    float acc[DEC_MAX_TOKENS] = {0.f, 0.f, 0.f, 0.f};
+    if (wv * 64 < n_pairs) {
+        const int4* e4 = (const int4*)s_e;
+        const f4* w4 = (const f4*)s_w;
+#pragma unroll 8
+        for (int q0 = 0; q0 < n_pairs; q0 += 4) {
+            const int4 ev = e4[q0 >> 2];
+            const f4 wq = w4[q0 >> 2];
+            const int ec[4] = {ev.x, ev.y, ev.z, ev.w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int q = q0 + c;
+                if (e >= 0 && q < n_pairs && ec[c] == e) {
+                    if (q < p) is_first = false;
+                    else acc[q / top_k] += wq[c];
+                }
+            }
+        }
     }
-    const bool is_first = (e >= 0 && first_p < 0);
     const uint64_t m = __ballot(is_first);
     if (lane == 0) s_wcount[wv] = __popcll(m);
     __syncthreads();
@@ -421,10 +444,6 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     if (is_first) {
         const int slot = before + __popcll(m & ((1ull << lane) - 1ull));
         P.ublob[slot] = s_tab[e];
-        /* weights of every token for this expert, in flat pair order */
-        float acc[DEC_MAX_TOKENS] = {0.f, 0.f, 0.f, 0.f};
-        for (int q = p; q < n_pairs; q++)
-            if (s_e[q] == e) acc[q / top_k] += s_w[q];
         for (int v = 0; v < DEC_MAX_TOKENS; v++) P.uw[slot * 4 + v] = acc[v] * poison;
     }
     if (p == 0) {
@@ -700,6 +719,7 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
      * min(4, ceil(nblk / NB)) waves and gsplit = ceil(nblk / (waves NB)) */
     const int xb0 = split * nw * NB;
     const int xlen = min(nw * NB, nblk - xb0);      /* blocks of this split */
+    if (xlen <= 0) return;   /* the launchers never make an empty split */
     const int b0 = xb0 + wave * NB, b1 = min(b0 + NB, nblk);
     const LdsMap L = lds_map(M, NT, min(K, nw * NB * 128), G, HZ, nw);
 
@@ -786,9 +806,20 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
                 up += red[((ww * NT + 1) * 16 + c) * M + v];
             }
             float* dst = P.gpart + ((size_t)tile_id * n_split + split) * 32 * M;
-            __hip_atomic_store(dst + o, g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(dst + 16 * M + o, up, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (FUSED || !P.gfinish) {
+                __hip_atomic_store(dst + o, g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(dst + 16 * M + o, up, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                dst[o] = g;
+                dst[16 * M + o] = up;
+            }
         }
+        /* With P.gfinish (separate gate/up launch), gateup_finish_kernel,
+         * launched next, adds the splits, so the workgroup ends with its
+         * stores: the hand-off round trips below hold the workgroup's
+         * slot for microseconds. */
+        if (!FUSED && P.gfinish) return;
         __builtin_amdgcn_s_waitcnt(0);   /* the wave's partial stores are acknowledged */
         int last = 0;
         if (lane == 0)
@@ -832,6 +863,34 @@ __device__ __forceinline__ void gateup_tile(const DecodeParams& P, int u, int rt
                                                 DEC_HCNT_STRIDE, 1,
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+/* After a K-split gate/up launch: h' of every (unique expert, row, token)
+ * from the splits' partial sums, added in split order from zero as the
+ * fused launch's last arrival adds them (so both give identical h'). One
+ * thread per output; grid (max_u * inter * M / 256). */
+template <int M>
+__global__ __launch_bounds__(256) void gateup_finish_kernel(const DecodeParams P) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int n_rt = P.inter / 16;
+    const int tile_id = i / (16 * M), o = i - tile_id * 16 * M;
+    const int u = tile_id / n_rt;
+    if (u >= *P.n_unique) return;
+    const int rt = tile_id - u * n_rt;
+    const int v = o % M, c = o / M;
+    const int n_split = P.gsplit;
+    const float* src = P.gpart + (size_t)tile_id * n_split * 32 * M;
+    float g = 0.0f, up = 0.0f;
+    for (int sp = 0; sp < n_split; sp++) {
+        g += src[sp * 32 * M + o];
+        up += src[sp * 32 * M + 16 * M + o];
+    }
+    const float h = silu_f(g) * up * P.uw[u * 4 + v];
+    const int r = rt * 16 + c;
+    const int e = r & 7;
+    const f16 hv = (f16)((e & 1) ? h * 0.0625f : h);
+    P.hperm[((size_t)v * P.max_u + u) * P.inter + (r & ~7) + perm_slot(e)] =
+        __builtin_bit_cast(uint16_t, hv);
 }
 
 /* grid (inter / (16 TILES) * gsplit, max_u): gate/up of unique expert
@@ -1158,6 +1217,14 @@ static FusedShape fused_shape(int nblk) {
     return f;
 }
 
+/* From this many tokens on, the separate gate/up launch hands its K-split
+ * partials to gateup_finish_kernel instead of a last-arrival round trip
+ * (measured, DeepSeek-V3 per layer: 4 tokens 187.3 -> 177.3 us; 3 tokens
+ * 131.9 -> 132.1 and 2 tokens 93.1 -> 94.1, where the extra launch costs
+ * what the round trips cost). */
+#ifndef DEC_FINISH_MIN_TOKENS
+#define DEC_FINISH_MIN_TOKENS 4
+#endif
 /* The first three regions sit at the same offsets for every layer shape,
  * so one workspace can serve calls of different shapes: the unique count
  * (offset 0) and the status word (DEC_STATUS_OFFSET), the routing epoch,
@@ -1197,7 +1264,11 @@ extern "C" size_t wisp_moe_decode_workspace_bytes(const WispExpertLayout* L, int
 }
 
 template <int M, int NG, int TILES, int NB, bool HZ>
-static void launch_gateup(const DecodeParams& P, int waves, hipStream_t s) {
+static hipError_t launch_gateup(const DecodeParams& P, int waves, hipStream_t s) {
+    /* every K split of a row tile covers at least one block */
+    const int nblk = P.hidden / 128, per = waves * NB;
+    if (P.gsplit < 1 || (P.gsplit - 1) * per >= nblk || P.gsplit * per < nblk)
+        return hipErrorInvalidValue;
     const int xk = P.hidden < waves * NB * 128 ? P.hidden : waves * NB * 128;
     const LdsMap L = lds_map(M, 2 * TILES, xk, P.hidden / P.gs, HZ, waves);
     auto k = gateup_kernel<M, NG, TILES, NB, HZ>;
@@ -1206,6 +1277,7 @@ static void launch_gateup(const DecodeParams& P, int waves, hipStream_t s) {
                                   L.bytes);
     hipLaunchKernelGGL(k, dim3(P.inter / (16 * TILES) * P.gsplit, P.max_u), dim3(64 * waves),
                        L.bytes, s, P);
+    return hipSuccess;
 }
 
 template <int M, int NG, bool HZ>
@@ -1238,36 +1310,35 @@ static void launch_fused(DecodeParams P, int waves, hipStream_t s) {
  * alone and the layer got slower (DeepSeek-V3 M=4: 281.6 against
  * 224.7 us), so M > 1 keeps two launches. */
 template <int M, int NG, bool HZ>
-static void launch_compute(const DecodeParams& P, hipStream_t s) {
+static hipError_t launch_compute(const DecodeParams& P, hipStream_t s) {
     const FusedShape f = fused_shape(P.hidden / 128);
     if constexpr (M == 1) {
         ev_before(EV_GATEUP, s);
         if (f.nb == 7) launch_fused<M, NG, 7, HZ>(P, f.waves, s);
         else launch_fused<M, NG, 8, HZ>(P, f.waves, s);
         ev_after(EV_GATEUP, s);
-        return;
+        return hipSuccess;
     }
     ev_before(EV_GATEUP, s);
-    if (f.nb == 7) launch_gateup<M, NG, 1, 7, HZ>(P, f.waves, s);
-    else launch_gateup<M, NG, 1, 8, HZ>(P, f.waves, s);
+    const hipError_t e = f.nb == 7 ? launch_gateup<M, NG, 1, 7, HZ>(P, f.waves, s)
+                                   : launch_gateup<M, NG, 1, 8, HZ>(P, f.waves, s);
+    if (e != hipSuccess) return e;
+    if (P.gfinish) {
+        const int n = P.max_u * P.inter * M;   /* a multiple of 256: inter % 128 == 0 */
+        hipLaunchKernelGGL(gateup_finish_kernel<M>, dim3(n / 256), dim3(256), 0, s, P);
+    }
     ev_after(EV_GATEUP, s);
     ev_before(EV_DOWN, s);
     launch_down<M, NG, HZ>(P, s);
     ev_after(EV_DOWN, s);
+    return hipSuccess;
 }
 
 template <int M>
-static void launch_ng(int ng, bool hz, const DecodeParams& P, hipStream_t s) {
-    if (ng == 1) {
-        if (hz) launch_compute<M, 1, true>(P, s);
-        else launch_compute<M, 1, false>(P, s);
-    } else if (ng == 2) {
-        if (hz) launch_compute<M, 2, true>(P, s);
-        else launch_compute<M, 2, false>(P, s);
-    } else {
-        if (hz) launch_compute<M, 4, true>(P, s);
-        else launch_compute<M, 4, false>(P, s);
-    }
+static hipError_t launch_ng(int ng, bool hz, const DecodeParams& P, hipStream_t s) {
+    if (ng == 1) return hz ? launch_compute<M, 1, true>(P, s) : launch_compute<M, 1, false>(P, s);
+    if (ng == 2) return hz ? launch_compute<M, 2, true>(P, s) : launch_compute<M, 2, false>(P, s);
+    return hz ? launch_compute<M, 4, true>(P, s) : launch_compute<M, 4, false>(P, s);
 }
 
 /* Bounded-wait settings of every launch: the poll limit, and an amount
@@ -1327,6 +1398,7 @@ static hipError_t decode_run(const void* const* d_expert_table, const void* d_sh
     P.hperm = (uint16_t*)(ws + w.hperm);
     P.part = (float*)(ws + w.part);
     P.gsplit = fused_shape(P.hidden / 128).gsplit;
+    P.gfinish = M >= DEC_FINISH_MIN_TOKENS && P.gsplit > 1;
     P.gcnt = (int*)(ws + w.gcnt);
     P.gpart = (float*)(ws + w.gpart);
     P.out32 = d_out_f32;
@@ -1362,11 +1434,12 @@ static hipError_t decode_run(const void* const* d_expert_table, const void* d_sh
     const int ng = P.gs >= 128 ? 1 : 128 / P.gs;
     const bool hz = P.has_zeros != 0;
     switch (M) {
-        case 1: launch_ng<1>(ng, hz, P, s); break;
-        case 2: launch_ng<2>(ng, hz, P, s); break;
-        case 3: launch_ng<3>(ng, hz, P, s); break;
-        default: launch_ng<4>(ng, hz, P, s); break;
+        case 1: e = launch_ng<1>(ng, hz, P, s); break;
+        case 2: e = launch_ng<2>(ng, hz, P, s); break;
+        case 3: e = launch_ng<3>(ng, hz, P, s); break;
+        default: e = launch_ng<4>(ng, hz, P, s); break;
     }
+    if (e != hipSuccess) return e;
     return hipGetLastError();
 }
 
