@@ -560,6 +560,14 @@ __device__ __forceinline__ void stage_groups(uint16_t* dst, const uint16_t* tab,
  * src + r * src_stride + 16 q and goes to dst + r * dst_stride + 16 q. Each
  * thread handles at most CNT pieces (ok() tells whether the copy fits);
  * out-of-range slots load a clamped in-range piece and store nothing. */
+/* One 16-byte global -> LDS load per lane: lane l's 16 bytes from src land
+ * at dst + 16 l (dst is the same for the whole wave). The load counts on
+ * vmcnt like any other; the LDS bytes are there once it has returned. */
+__device__ __forceinline__ void lds_load16(const void* src, void* dst) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+}
+
 template <int CNT>
 struct Stage16 {
     u4 v[CNT];
@@ -938,8 +946,8 @@ __host__ __device__ inline LdsMap down_wave_map(int M, int gmax, bool hz, int wa
     return L;
 }
 
-/* Workgroup (row tile rt, chunk q) of nw waves covers wave units
- * [nw q, nw q + nw) of the concatenated K axis and
+/* Down part of the fused launch. Workgroup (row tile rt, chunk q) of nw
+ * waves covers wave units [nw q, nw q + nw) of the concatenated K axis and
  * computes part[q][v][row] = sum over its units of down_u[row, unit] .
  * h'_u[v][unit] (routing weight already folded into h'). The last of the row
  * tile's n_q workgroups to arrive adds all of the tile's partials in chunk
@@ -947,11 +955,10 @@ __host__ __device__ inline LdsMap down_wave_map(int M, int gmax, bool hz, int wa
  * needs no cache write-back: partials are stored and loaded with
  * device-coherent accesses, every store is acknowledged before the arrival
  * is counted, and the counters are zeroed by the prep kernel of the same
- * call. In the fused launch (FUSED) each wave first waits until every
- * gate/up workgroup of its unit has counted itself (a bounded poll: those
- * workgroups come earlier in the grid and wait on nothing), then reads h'
- * with device-coherent loads. */
-template <int M, int NG, bool HZ, bool FUSED>
+ * call. Each wave first waits until every gate/up workgroup of its unit has
+ * counted itself (a bounded poll: those workgroups come earlier in the grid
+ * and wait on nothing), then reads h' with device-coherent loads. */
+template <int M, int NG, bool HZ>
 __device__ __forceinline__ void down_tile(const DecodeParams& P, int q, int rt, uint8_t* smem) {
     constexpr int NB = DEC_UNIT_BLOCKS;
     constexpr int GMAX = NB * NG;
@@ -988,15 +995,12 @@ __device__ __forceinline__ void down_tile(const DecodeParams& P, int q, int rt, 
 #pragma unroll
     for (int v = 0; v < M; v++) tot[0][v] = 0.0f;
     if (live) {
-    /* Order of issue (loads return in order). Alone: the unit's h' and
-     * scales, then its weights, so the LDS writes wait only for the former.
-     * Fused: the first poll of the unit's counter, the scales and the
-     * weights, then the wait for the counter (its load returns first), then
-     * h' (after the poll, so it sees every gate/up store): the poll's round
-     * trip overlaps the weight stream instead of preceding it. */
-    int hc = 0;
-    if (FUSED)
-        hc = __hip_atomic_load(P.hcnt + gu * DEC_HCNT_STRIDE, __ATOMIC_RELAXED,
+    /* Order of issue (loads return in order): the first poll of the unit's
+     * counter, the scales and the weights, then the wait for the counter
+     * (its load returns first), then h' (after the poll, so it sees every
+     * gate/up store): the poll's round trip overlaps the weight stream
+     * instead of preceding it. */
+    int hc = __hip_atomic_load(P.hcnt + gu * DEC_HCNT_STRIDE, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
     constexpr int XC = NB / 4;   /* 16-byte pieces of the unit's h' per lane and token */
     u4 xv[M][XC];
@@ -1008,19 +1012,15 @@ __device__ __forceinline__ void down_tile(const DecodeParams& P, int q, int rt, 
             for (int c = 0; c < XC; c++) {
                 const int i = min(lane + 64 * c, nb * 16 - 1);
                 const uint16_t* src = hsrc + (size_t)v * P.max_u * K + i * 8;
-                if (FUSED) {
-                    const uint64_t a = __hip_atomic_load((const uint64_t*)src, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-                    const uint64_t b = __hip_atomic_load((const uint64_t*)src + 1,
-                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    xv[v][c] = (u4){(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b,
-                                    (uint32_t)(b >> 32)};
-                } else {
-                    xv[v][c] = *(const u4*)src;
-                }
+                const uint64_t a = __hip_atomic_load((const uint64_t*)src, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t b = __hip_atomic_load((const uint64_t*)src + 1, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+                xv[v][c] = (u4){(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b,
+                                (uint32_t)(b >> 32)};
             }
     };
-    if (!FUSED) load_h();
+    uint16_t* xs = (uint16_t*)(smem + L.x_off);
     constexpr int SCNT = (16 * GMAX + 63) / 64;
     uint16_t sv[SCNT], zv[SCNT];
     const uint16_t* stab = (const uint16_t*)(blob + P.s_off[2]);
@@ -1037,22 +1037,18 @@ __device__ __forceinline__ void down_tile(const DecodeParams& P, int q, int rt, 
     const uint8_t* wp[1] = {blob + P.p_off[2] + (size_t)(r0 + col) * (K / 2) + 16 * j};
     u4 w[NB][1];
     load_blocks<1, NB>(wp, lb0, lb1 - 1, w);
-    bool gave_up = false;
-    if (FUSED) {
-        /* h' of this unit: written by nb * 8 gate/up workgroups */
-        const int want = nb * 8 + P.poll_extra;
-        int polls = 0;
-        while (hc < want && polls < P.poll_limit) {
-            __builtin_amdgcn_s_sleep(DEC_POLL_SLEEP);
-            polls++;
-            hc = __hip_atomic_load(P.hcnt + gu * DEC_HCNT_STRIDE, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        }
-        gave_up = hc < want;
-        load_h();
+    /* h' of this unit: written by nb * 8 gate/up workgroups */
+    const int want = nb * 8 + P.poll_extra;
+    int polls = 0;
+    while (hc < want && polls < P.poll_limit) {
+        __builtin_amdgcn_s_sleep(DEC_POLL_SLEEP);
+        polls++;
+        hc = __hip_atomic_load(P.hcnt + gu * DEC_HCNT_STRIDE, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     }
+    const bool gave_up = hc < want;
+    load_h();
 
-    uint16_t* xs = (uint16_t*)(smem + L.x_off);
 #pragma unroll
     for (int v = 0; v < M; v++)
 #pragma unroll
@@ -1128,11 +1124,140 @@ __device__ __forceinline__ void down_tile(const DecodeParams& P, int q, int rt, 
     }
 }
 
-/* grid (hidden / 16, n_q_max), DN_WAVES waves: the down projection alone. */
+/* LDS image of a workgroup of the separate down launch: x [M][1024 + 32]
+ * (the unit's h', shared by the waves), then per wave sc [16][GMAX] and
+ * zc [16][GMAX] (its row tile's raw scale and zero bits). */
+__host__ __device__ inline LdsMap down_rows_map(int M, int gmax, bool hz, int wave) {
+    LdsMap L;
+    L.XR = DEC_UNIT_BLOCKS * 128 + 32;
+    L.GS = gmax;
+    L.x_off = 0;
+    const int xb = (M * L.XR * 2 + 15) & ~15;
+    const int tb = (16 * gmax * 2 + 15) & ~15;
+    const int pw = hz ? 2 * tb : tb;
+    L.sc_off = xb + wave * pw;
+    L.zc_off = L.sc_off + tb;
+    L.red_off = 0;
+    L.bytes = xb + DN_WAVES * pw;
+    return L;
+}
+
+/* The down projection alone (two launches): workgroup (row group
+ * blockIdx.x, wave unit blockIdx.y) stages the unit's h' once in LDS for
+ * its DN_WAVES waves, and wave w computes rows r = 16 (DN_WAVES blockIdx.x
+ * + w) + [0, 16) of part[unit][v][r] = down_u[r, unit's K range] .
+ * h'_u[v][unit's K range] (routing weight folded into h'). It stores them
+ * and ends: no workgroup waits on another, and down_combine_kernel adds the
+ * units in unit order. Sharing h' across the row tiles of a unit keeps the
+ * workgroup's LDS small (10 KB for 4 tokens), so LDS no longer caps the
+ * workgroups per CU below what the registers allow. */
 template <int M, int NG, bool HZ>
-__global__ __launch_bounds__(64 * DN_WAVES) void down_kernel(const DecodeParams P) {
+__global__ __launch_bounds__(64 * DN_WAVES)
+__attribute__((amdgpu_waves_per_eu(NG == 1 ? (HZ ? 4 : 5) : (NG == 2 && !HZ ? 2 : 1))))
+void down_kernel(const DecodeParams P) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    down_tile<M, NG, HZ, false>(P, blockIdx.y, blockIdx.x, smem);
+    constexpr int NB = DEC_UNIT_BLOCKS;
+    constexpr int GMAX = NB * NG;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, j = lane >> 4;
+    const int K = P.inter, H = P.hidden;
+    const int nblk = K >> 7;
+    const int gu = blockIdx.y;
+    const int u = min(gu / P.upe, P.max_u - 1);
+    /* both loads in one round trip (slot u < max_u always exists) */
+    const int n_u = *P.n_unique;
+    const uint8_t* blob = P.ublob[u];
+    if (gu >= n_u * P.upe) return;
+    const int r0 = (blockIdx.x * DN_WAVES + wave) * 16;
+    const int lb0 = (gu - u * P.upe) * NB;
+    const int lb1 = min(lb0 + NB, nblk);
+    const int nb = lb1 - lb0;
+    const int G = K / P.gs;
+    const int g_lo = (lb0 * NG) >> P.gshift;
+    const int gn = (((lb1 * NG) - 1) >> P.gshift) + 1 - g_lo;
+    const LdsMap L = down_rows_map(M, GMAX, HZ, wave);
+
+    /* Order of issue (loads return in order): the unit's h' straight into
+     * LDS (2 M pieces of 1 KB spread over the waves; pieces past a short
+     * last unit repeat its last 16 bytes, read only by padding blocks of
+     * zero scale), the row tile's scales, then its weights. */
+    uint16_t* xs = (uint16_t*)(smem + L.x_off);
+    const uint16_t* hsrc = P.hperm + (size_t)u * K + lb0 * 128;
+    constexpr int PCS = (2 * M + DN_WAVES - 1) / DN_WAVES;
+#pragma unroll
+    for (int k = 0; k < PCS; k++) {
+        const int pc = wave + k * DN_WAVES;
+        if (pc < 2 * M) {
+            const int v = pc >> 1, c = pc & 1;
+            const int i = min(lane + 64 * c, nb * 16 - 1);
+            lds_load16(hsrc + (size_t)v * P.max_u * K + i * 8,
+                       (uint8_t*)(xs + v * L.XR) + 1024 * c);
+        }
+    }
+    constexpr int SCNT = (16 * GMAX + 63) / 64;
+    uint16_t sv[SCNT], zv[SCNT];
+    const uint16_t* stab = (const uint16_t*)(blob + P.s_off[2]);
+    const uint16_t* ztab = (const uint16_t*)(blob + P.z_off[2]);
+#pragma unroll
+    for (int c = 0; c < SCNT; c++) {
+        const int i = min(lane + 64 * c, 16 * gn - 1);
+        const int rr = i / gn, gg = i - rr * gn;
+        const size_t at = (size_t)(r0 + rr) * G + g_lo + gg;
+        sv[c] = gptr(stab)[at];
+        zv[c] = HZ ? gptr(ztab)[at] : (uint16_t)0;
+    }
+    __builtin_amdgcn_sched_barrier(0);   /* the scale loads stay ahead of the weights */
+    const uint8_t* wp[1] = {blob + P.p_off[2] + (size_t)(r0 + col) * (K / 2) + 16 * j};
+    u4 w[NB][1];
+    load_blocks<1, NB>(wp, lb0, lb1 - 1, w);
+
+    /* the scales return after h' (in order), so once they are written
+     * every wave's h' pieces are in LDS */
+    uint16_t* ss = (uint16_t*)(smem + L.sc_off);
+    uint16_t* zs = (uint16_t*)(smem + L.zc_off);
+#pragma unroll
+    for (int c = 0; c < SCNT; c++) {
+        const int i = lane + 64 * c;
+        if (i < 16 * gn) {
+            const int rr = i / gn, gg = i - rr * gn;
+            ss[rr * GMAX + gg] = sv[c];
+            if (HZ) zs[rr * GMAX + gg] = zv[c];
+        }
+    }
+    __syncthreads();
+
+    float tot[1][M];
+#pragma unroll
+    for (int v = 0; v < M; v++) tot[0][v] = 0.0f;
+    compute_blocks<M, NG, 1, NB, HZ>(w, smem, L, lb0, lb1, lb0, g_lo, P.gshift, col, j,
+                                     P.m_lo, P.m_hi, P.one024, tot);
+    if (lane < 16) {
+#pragma unroll
+        for (int v = 0; v < M; v++) P.part[((size_t)gu * M + v) * H + r0 + col] = tot[0][v];
+    }
+}
+
+/* After the separate down launch: out[v][r] = the sum of part[unit][v][r]
+ * over the call's wave units, in unit order from zero. One thread per
+ * output. */
+template <int M>
+__global__ __launch_bounds__(256) void down_combine_kernel(const DecodeParams P) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= M * P.hidden) return;
+    const int n_units = *P.n_unique * P.upe;
+    const float* src = P.part + i;
+    const size_t stride = (size_t)M * P.hidden;
+    constexpr int MAXQ = 32;
+    float y = 0.0f;
+    for (int q0 = 0; q0 < n_units; q0 += MAXQ) {
+        float t[MAXQ];
+#pragma unroll
+        for (int qq = 0; qq < MAXQ; qq++)
+            t[qq] = q0 + qq < n_units ? src[(size_t)(q0 + qq) * stride] : 0.0f;
+#pragma unroll
+        for (int qq = 0; qq < MAXQ; qq++) y += t[qq];
+    }
+    store_out(P, i, y);
 }
 
 /* One launch for gate/up and down: the first max_u * inter / 16 * gsplit
@@ -1155,7 +1280,7 @@ __global__ __launch_bounds__(64 * DEC_MAX_WAVES) void expert_kernel(const Decode
         gateup_tile<M, NG, 1, NB, HZ, true>(P, u, r / P.gsplit, r % P.gsplit, smem);
     } else {
         const int d = b - n_gu, n_ro = P.hidden / 16;
-        down_tile<M, NG, HZ, true>(P, d / n_ro, d % n_ro, smem);
+        down_tile<M, NG, HZ>(P, d / n_ro, d % n_ro, smem);
     }
 }
 
@@ -1281,11 +1406,15 @@ static hipError_t launch_gateup(const DecodeParams& P, int waves, hipStream_t s)
 }
 
 template <int M, int NG, bool HZ>
-static void launch_down(DecodeParams P, hipStream_t s) {
-    P.n_q_max = (P.max_u * P.upe + DN_WAVES - 1) / DN_WAVES;
-    const LdsMap L = down_wave_map(M, DEC_UNIT_BLOCKS * NG, HZ, 0, DN_WAVES);
+static hipError_t launch_down(const DecodeParams& P, hipStream_t s) {
+    if (P.hidden % (16 * DN_WAVES) != 0) return hipErrorInvalidValue;
+    const LdsMap L = down_rows_map(M, DEC_UNIT_BLOCKS * NG, HZ, 0);
     auto k = down_kernel<M, NG, HZ>;
-    hipLaunchKernelGGL(k, dim3(P.hidden / 16, P.n_q_max), dim3(64 * DN_WAVES), L.bytes, s, P);
+    hipLaunchKernelGGL(k, dim3(P.hidden / (16 * DN_WAVES), P.max_u * P.upe), dim3(64 * DN_WAVES),
+                       L.bytes, s, P);
+    hipLaunchKernelGGL(down_combine_kernel<M>, dim3((M * P.hidden + 255) / 256), dim3(256), 0, s,
+                       P);
+    return hipSuccess;
 }
 
 /* gate/up and down in one launch (expert_kernel) */
@@ -1329,7 +1458,8 @@ static hipError_t launch_compute(const DecodeParams& P, hipStream_t s) {
     }
     ev_after(EV_GATEUP, s);
     ev_before(EV_DOWN, s);
-    launch_down<M, NG, HZ>(P, s);
+    const hipError_t ed = launch_down<M, NG, HZ>(P, s);
+    if (ed != hipSuccess) return ed;
     ev_after(EV_DOWN, s);
     return hipSuccess;
 }
