@@ -280,6 +280,12 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     /* NaN when the routing wait gave up (multiplies every routing weight:
      * x * 1 is exact, so it changes nothing otherwise) */
     float poison = 1.0f;
+    /* the selection bias of the expert this thread ranks in topk_one_token
+     * (64 (wave % 4) + lane), loaded before the wait for the logits */
+    const bool has_bias = R.mode != 0 && R.kind == WISP_ROUTER_SIGMOID && R.bias != nullptr;
+    const int bias_row = (wv & 3) * 64 + lane;
+    const float bias_e =
+        has_bias && bias_row < n_experts ? half_bits_to_float(R.bias[bias_row]) : 0.0f;
     if (R.mode != 0) {
         /* dynamic LDS: 64-bit selection keys (scratch of the top-k), then
          * scores [M][n_experts] (the raw logits first) */
@@ -295,18 +301,41 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
             const uint32_t tok =
                 __hip_atomic_load(R.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
             const uint32_t want = tok + (uint32_t)P.poll_extra;
+            /* all of this thread's words in one round trip, then only the
+             * ones not yet tagged with this call again */
+            constexpr int WPT = DEC_MAX_TOKENS * DEC_ROUTE_MAX_EXPERTS / DEC_PREP_THREADS;
+            const int n_words = M * n_experts;
+            uint64_t v[WPT];
+#pragma unroll
+            for (int k = 0; k < WPT; k++) {
+                const int i = threadIdx.x + k * DEC_PREP_THREADS;
+                v[k] = i < n_words ? __hip_atomic_load(R.words + i, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT)
+                                   : (uint64_t)want << 32;
+            }
+            auto all_tagged = [&]() {
+                bool ok = true;
+#pragma unroll
+                for (int k = 0; k < WPT; k++) ok &= (uint32_t)(v[k] >> 32) == want;
+                return ok;
+            };
             int polls = 0;
-            bool gave_up = false;
-            for (int i = threadIdx.x; i < M * n_experts; i += blockDim.x) {
-                uint64_t v = __hip_atomic_load(R.words + i, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-                while ((uint32_t)(v >> 32) != want && polls < P.poll_limit) {
-                    __builtin_amdgcn_s_sleep(8);
-                    polls++;
-                    v = __hip_atomic_load(R.words + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            while (!all_tagged() && polls < P.poll_limit) {
+                __builtin_amdgcn_s_sleep(8);
+                polls++;
+#pragma unroll
+                for (int k = 0; k < WPT; k++) {
+                    const int i = threadIdx.x + k * DEC_PREP_THREADS;
+                    if ((uint32_t)(v[k] >> 32) != want)
+                        v[k] = __hip_atomic_load(R.words + i, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
                 }
-                gave_up |= (uint32_t)(v >> 32) != want;
-                s_sc[i] = __uint_as_float((uint32_t)v);
+            }
+            const bool gave_up = !all_tagged();
+#pragma unroll
+            for (int k = 0; k < WPT; k++) {
+                const int i = threadIdx.x + k * DEC_PREP_THREADS;
+                if (i < n_words) s_sc[i] = __uint_as_float((uint32_t)v[k]);
             }
             if (__syncthreads_or(gave_up)) {
                 poison = __builtin_nanf("");
@@ -354,9 +383,8 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
              * waves, two tokens per pass, one barrier per pass */
             const int grp = wv >> 2;
             const int ka = prep_key_slots(n_experts);
-            const uint16_t* sbias = R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr;
             if (M == 1) {
-                topk_one_token(s_sc, sbias, R.logits, s_ck, s_cand[0], s_sel[0], s_red,
+                topk_one_token(s_sc, has_bias, bias_e, R.logits, s_ck, s_cand[0], s_sel[0], s_red,
                                n_experts, top_k, R.kind, grp == 0 ? (wv & 3) : -1,
                                one_token_list);
                 return;
@@ -370,7 +398,8 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
                         s_w[t * top_k + lane] = w;
                     }
                 };
-                topk_one_token(s_sc + tt * n_experts, sbias, R.logits + (size_t)tt * n_experts,
+                topk_one_token(s_sc + tt * n_experts, has_bias, bias_e,
+                               R.logits + (size_t)tt * n_experts,
                                s_ck + grp * ka, s_cand[grp], s_sel[grp], s_red + 8 * grp,
                                n_experts, top_k, R.kind, t < M ? (wv & 3) : -1, to_lds);
                 __syncthreads();   /* the next pass reuses the groups' scratch */
@@ -408,30 +437,24 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
         e = s_e[p];
         if (e < 0 || e >= n_experts) e = -1;
     }
-    /* Every pair against every pair, lane-parallel: the pair list is read
-     * 4 entries at a time with every lane reading the same 16 bytes (a
-     * broadcast), unrolled so the reads are in flight together; a loop of
-     * dependent single reads costs an LDS round trip per pair. A pair is
-     * its expert's first when no earlier pair names the same expert; the
-     * first one also sums every token's weight for the expert, in flat
-     * pair order. Waves past the pairs skip the scan (the trip count is
-     * uniform within a wave). */
+    /* Every pair against every pair, lane-parallel (every lane reads the
+     * same pair: an LDS broadcast), branch-free, token by token so each
+     * token's sum has a fixed register. A pair is its expert's first when
+     * no earlier pair names the same expert; the first one also sums every
+     * token's weight for the expert, in flat pair order (adding +0 for the
+     * other pairs changes no sum: each starts at +0). Waves past the pairs
+     * skip the scan (the trip count is uniform within a wave). */
     bool is_first = e >= 0;
     float acc[DEC_MAX_TOKENS] = {0.f, 0.f, 0.f, 0.f};
     if (wv * 64 < n_pairs) {
-        const int4* e4 = (const int4*)s_e;
-        const f4* w4 = (const f4*)s_w;
-#pragma unroll 8
-        for (int q0 = 0; q0 < n_pairs; q0 += 4) {
-            const int4 ev = e4[q0 >> 2];
-            const f4 wq = w4[q0 >> 2];
-            const int ec[4] = {ev.x, ev.y, ev.z, ev.w};
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const int q = q0 + c;
-                if (e >= 0 && q < n_pairs && ec[c] == e) {
-                    if (q < p) is_first = false;
-                    else acc[q / top_k] += wq[c];
+        for (int t = 0; t < DEC_MAX_TOKENS; t++) {
+            if (t < M) {
+                for (int jj = 0; jj < top_k; jj++) {
+                    const int q = t * top_k + jj;
+                    const bool hit = s_e[q] == e;
+                    is_first = is_first && !(hit && q < p);
+                    acc[t] += hit && q >= p ? s_w[q] : 0.0f;
                 }
             }
         }

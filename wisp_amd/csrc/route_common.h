@@ -290,9 +290,11 @@ __device__ __forceinline__ void topk_wave_small(const float* lg, const uint16_t*
  * the same formulas, with the softmax denominator summed per wave (rescaled
  * to the global maximum), so they agree to rounding. Group LDS: s_key 256
  * u64, s_cand 64 u64 (both 16-byte aligned), s_sel 16 ints, s_red 8
- * floats. */
+ * floats. bias_e: the fp16 selection bias of expert 64 wl + lane as a
+ * float, loaded by the caller ahead of the logits (used when has_bias,
+ * for SIGMOID). */
 template <typename Emit>
-__device__ __forceinline__ void topk_one_token(const float* lg, const uint16_t* __restrict__ bias,
+__device__ __forceinline__ void topk_one_token(const float* lg, bool has_bias, float bias_e,
                                                float* scores_out, uint64_t* s_key,
                                                uint64_t* s_cand, int* s_sel, float* s_red,
                                                int n_experts, int top_k, int kind, int wl,
@@ -304,7 +306,7 @@ __device__ __forceinline__ void topk_one_token(const float* lg, const uint16_t* 
     const bool act = grp && e < n_experts;
     const float l = act ? lg[e] : -INFINITY;
     const float sg = sig ? 1.0f / (1.0f + __expf(-l)) : 0.0f;
-    const float key = (sig && bias && act) ? sg + half_bits_to_float(bias[e]) : (sig ? sg : l);
+    const float key = (sig && has_bias && act) ? sg + bias_e : (sig ? sg : l);
     const uint64_t ce = act ? route_composite(key, e) : 0ull;
     if (grp) {
         s_key[e] = ce;
