@@ -437,28 +437,45 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
         e = s_e[p];
         if (e < 0 || e >= n_experts) e = -1;
     }
-    /* Every pair against every pair, lane-parallel (every lane reads the
-     * same pair: an LDS broadcast), branch-free, token by token so each
-     * token's sum has a fixed register. A pair is its expert's first when
-     * no earlier pair names the same expert; the first one also sums every
-     * token's weight for the expert, in flat pair order (adding +0 for the
-     * other pairs changes no sum: each starts at +0). Waves past the pairs
-     * skip the scan (the trip count is uniform within a wave). */
-    bool is_first = e >= 0;
+    /* Every pair against every pair, lane-parallel: every lane reads the
+     * same pair (an LDS broadcast), token by token so each token's sum has
+     * a fixed register. A pair is its expert's first when no earlier pair
+     * names the same expert; the first one also sums every token's weight
+     * for the expert, in flat pair order. Up to 8 slots per token: fully
+     * unrolled with the reads unconditional (in the arrays' bounds) and
+     * integer masks instead of conditions, so the reads are all in flight
+     * together and nothing branches; a masked weight adds +0, which
+     * changes no sum (each starts at +0). Waves past the pairs skip the
+     * scan (the trip count is uniform within a wave). */
     float acc[DEC_MAX_TOKENS] = {0.f, 0.f, 0.f, 0.f};
+    int seen_before = 0;
     if (wv * 64 < n_pairs) {
+        if (top_k <= 8) {
 #pragma unroll
-        for (int t = 0; t < DEC_MAX_TOKENS; t++) {
-            if (t < M) {
-                for (int jj = 0; jj < top_k; jj++) {
-                    const int q = t * top_k + jj;
-                    const bool hit = s_e[q] == e;
-                    is_first = is_first && !(hit && q < p);
-                    acc[t] += hit && q >= p ? s_w[q] : 0.0f;
+            for (int t = 0; t < DEC_MAX_TOKENS; t++)
+#pragma unroll
+                for (int c = 0; c < 8; c++) {
+                    const int q = t * top_k + c;
+                    const int eq = s_e[q];
+                    const float wq = s_w[q];
+                    const int hit = -(int)((t < M) & (c < top_k) & (eq == e));
+                    const int before = -(int)(q < p);
+                    seen_before |= hit & before;
+                    acc[t] += __int_as_float(__float_as_int(wq) & hit & ~before);
+                }
+        } else {
+            for (int q = 0; q < n_pairs; q++) {
+                const int t = q / top_k;
+                const bool hit = s_e[q] == e;
+                if (hit && q < p) seen_before = 1;
+                if (hit && q >= p) {
+                    for (int v = 0; v < DEC_MAX_TOKENS; v++)
+                        if (v == t) acc[v] += s_w[q];
                 }
             }
         }
     }
+    const bool is_first = e >= 0 && seen_before == 0;
     const uint64_t m = __ballot(is_first);
     if (lane == 0) s_wcount[wv] = __popcll(m);
     __syncthreads();
