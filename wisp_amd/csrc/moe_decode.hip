@@ -123,10 +123,10 @@ __host__ __device__ constexpr int prep_key_slots(int n_experts) {
     return n_experts > 256 ? align_up_dev(n_experts, 64) : 256;
 }
 
-/* LDS of the 64-bit selection keys: two arrays, one per wave group of the
- * grouped selection. */
+/* LDS of the 64-bit selection keys: four arrays, one per token of the
+ * grouped selection (two groups of four waves, two tokens each). */
 __host__ __device__ constexpr int prep_key_bytes(int n_experts) {
-    return 2 * prep_key_slots(n_experts) * 8;
+    return DEC_MAX_TOKENS * prep_key_slots(n_experts) * 8;
 }
 
 /* Dynamic LDS of the prep kernel in routing modes 1 and 3: selection keys
@@ -179,8 +179,8 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     __shared__ int s_wcount[NWV];
     __shared__ const uint8_t* s_tab[DEC_ROUTE_MAX_EXPERTS];
     __shared__ float s_red[32];
-    __shared__ __attribute__((aligned(16))) uint64_t s_cand[2][64];
-    __shared__ int s_sel[2][DEC_MAX_TOPK];
+    __shared__ __attribute__((aligned(16))) uint64_t s_cand[DEC_MAX_TOKENS][64];
+    __shared__ int s_sel[DEC_MAX_TOKENS][DEC_MAX_TOPK];
     const int M = P.M;
     const int n_pairs = M * top_k;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -389,21 +389,26 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
                                one_token_list);
                 return;
             }
-            for (int t0 = 0; t0 < M; t0 += NWV / 4) {
-                const int t = t0 + grp;
-                const int tt = t < M ? t : 0;
-                auto to_lds = [&](int e, float w) {
-                    if (lane < top_k) {
-                        s_e[t * top_k + lane] = e;
-                        s_w[t * top_k + lane] = w;
-                    }
-                };
-                topk_one_token(s_sc + tt * n_experts, has_bias, bias_e,
-                               R.logits + (size_t)tt * n_experts,
-                               s_ck + grp * ka, s_cand[grp], s_sel[grp], s_red + 8 * grp,
-                               n_experts, top_k, R.kind, t < M ? (wv & 3) : -1, to_lds);
-                __syncthreads();   /* the next pass reuses the groups' scratch */
-            }
+            /* group g selects tokens g and g + 2 in one pass */
+            static_assert(DEC_MAX_TOKENS == 2 * (NWV / 4), "two tokens per group");
+            const int ta = grp, tb = grp + 2;
+            const bool live[2] = {ta < M, tb < M};
+            const int ca = live[0] ? ta : 0, cb = live[1] ? tb : 0;
+            const float* lg[2] = {s_sc + ca * n_experts, s_sc + cb * n_experts};
+            float* so[2] = {R.logits + (size_t)ca * n_experts, R.logits + (size_t)cb * n_experts};
+            uint64_t* sk[2] = {s_ck + ta * ka, s_ck + tb * ka};
+            uint64_t* sc2[2] = {s_cand[ta], s_cand[tb]};
+            int* ss2[2] = {s_sel[ta], s_sel[tb]};
+            float* sr[2] = {s_red + 8 * ta, s_red + 8 * tb};
+            auto to_lds = [&](int k, int e, float w) {
+                const int t = k == 0 ? ta : tb;
+                if (lane < top_k) {
+                    s_e[t * top_k + lane] = e;
+                    s_w[t * top_k + lane] = w;
+                }
+            };
+            topk_tokens<2>(lg, live, has_bias, bias_e, so, sk, sc2, ss2, sr, n_experts, top_k,
+                           R.kind, wv & 3, to_lds);
         } else {
             for (int t = 0; t < M; t++)
                 topk_block(s_sc + t * n_experts, R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr,

@@ -357,6 +357,87 @@ __device__ __forceinline__ void topk_one_token(const float* lg, bool has_bias, f
     if (act) scores_out[e] = sig ? sg : __expf(l - mx) * inv;
 }
 
+/* topk_one_token for NT tokens at once per group of four waves: the same
+ * steps and formulas for each token, with one barrier for all of them, so
+ * the tokens' dependent chains (rank reads, exponentials, reductions) run
+ * side by side. Token k uses lg[k], scores_out[k] and its own scratch
+ * s_key[k], s_cand[k], s_sel[k], s_red[k] (as topk_one_token's); a token
+ * with live[k] false does nothing but still takes part in the barrier.
+ * emit(k, e, w) as topk_one_token's emit(e, w), for wave wl = 0. */
+template <int NT, typename Emit>
+__device__ __forceinline__ void topk_tokens(const float* const (&lg)[NT], const bool (&live)[NT],
+                                            bool has_bias, float bias_e,
+                                            float* const (&scores_out)[NT],
+                                            uint64_t* const (&s_key)[NT],
+                                            uint64_t* const (&s_cand)[NT],
+                                            int* const (&s_sel)[NT], float* const (&s_red)[NT],
+                                            int n_experts, int top_k, int kind, int wl,
+                                            Emit emit) {
+    const bool sig = kind == WISP_ROUTER_SIGMOID;
+    const int lane = threadIdx.x & 63;
+    const bool grp = wl >= 0 && wl < 4;
+    const int e = (grp ? wl : 0) * 64 + lane;
+    float l[NT], sg[NT];
+#pragma unroll
+    for (int k = 0; k < NT; k++) {
+        const bool act = grp && live[k] && e < n_experts;
+        l[k] = act ? lg[k][e] : -INFINITY;
+        sg[k] = sig ? 1.0f / (1.0f + __expf(-l[k])) : 0.0f;
+        const float key = (sig && has_bias && act) ? sg[k] + bias_e : (sig ? sg[k] : l[k]);
+        const uint64_t ce = act ? route_composite(key, e) : 0ull;
+        if (grp && live[k]) {
+            s_key[k][e] = ce;
+            const int rank = lds_rank<32>(s_key[k] + wl * 64, ce);
+            if (lane < top_k) s_cand[k][wl * top_k + lane] = 0ull;
+            if (act && (ce >> 32) != 0 && rank < top_k) s_cand[k][wl * top_k + rank] = ce;
+            if (!sig) {
+                const float wmax = wave_max_dpp(l[k]);
+                const float wsum = wave_sum_dpp(act ? __expf(l[k] - wmax) : 0.0f);
+                if (lane == 0) {
+                    s_red[k][wl] = wmax;
+                    s_red[k][4 + wl] = wsum;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    if (!grp) return;
+#pragma unroll
+    for (int k = 0; k < NT; k++) {
+        if (!live[k]) continue;
+        float mx = 0.0f, inv = 1.0f;
+        if (!sig) {
+            mx = fmaxf(fmaxf(s_red[k][0], s_red[k][1]), fmaxf(s_red[k][2], s_red[k][3]));
+            float den = 0.0f;
+            for (int q = 0; q < 4; q++)
+                if (s_red[k][4 + q] != 0.0f) den += s_red[k][4 + q] * __expf(s_red[k][q] - mx);
+            inv = 1.0f / (den > 0.0f ? den : 1.0f);
+        }
+        if (wl == 0) {
+            const int nc = 4 * top_k;
+            const uint64_t cc = lane < nc ? s_cand[k][lane] : 0ull;
+            const u64x2* c2 = (const u64x2*)s_cand[k];
+            int rank = 0;
+#pragma unroll 8
+            for (int q = 0; q < nc / 2; q++) {
+                const u64x2 v = c2[q];
+                rank += (v.x > cc) + (v.y > cc);
+            }
+            if (lane < top_k) s_sel[k][lane] = -1;
+            if (lane < nc && (cc >> 32) != 0 && rank < top_k) s_sel[k][rank] = (int)~(uint32_t)cc;
+            const int sel_e = lane < top_k ? s_sel[k][lane] : -1;
+            float v = 0.0f;
+            if (sel_e >= 0) {
+                const float ls = lg[k][sel_e];
+                v = sig ? 1.0f / (1.0f + __expf(-ls)) : __expf(ls - mx) * inv;
+            }
+            const float wsum = wave_sum_dpp(v);
+            emit(k, sel_e, wsum > 0.0f ? v / wsum : v);
+        }
+        if (e < n_experts) scores_out[k][e] = sig ? sg[k] : __expf(l[k] - mx) * inv;
+    }
+}
+
 /* All threads of the workgroup, one token. lg: the token's raw logits
  * [n_experts] (LDS or global; for SOFTMAX they already include the bias).
  * s_ck: LDS scratch of n_experts uint64, 16-byte aligned; s_sc: LDS
