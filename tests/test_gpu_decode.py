@@ -74,6 +74,23 @@ def test_small_variants(shared, zeros):
     run_decode(77, 384, 640, 128, n_exp, k, M, shared, zeros, idx, w)
 
 
+@pytest.mark.parametrize("top_k", [8, 12])
+def test_repeated_expert_within_token(top_k):
+    """Caller-given slots that name one expert twice in one token (and a
+    skipped slot): the unique list adds both weights in slot order, as the
+    oracle adds both contributions; top_k 12 takes the unique list's
+    general scan (more than 8 slots per token)."""
+    print(f"decode repeated expert top_k={top_k}", flush=True)
+    rng = np.random.default_rng(40 + top_k)
+    n_exp, M = 32, 3
+    idx = synth.uniform_topk(rng, M, n_exp, top_k)
+    idx[1, 3] = idx[1, 0]                # same expert twice in token 1
+    idx[2, 5] = -1                       # skipped slot
+    idx[0, 1] = idx[2, 2]                # expert shared between tokens
+    w = synth.route_weights(rng, M, top_k)
+    run_decode(500 + top_k, 256, 512, 128, n_exp, top_k, M, True, False, idx, w)
+
+
 def test_fp32_input_and_accumulate():
     rng = np.random.default_rng(8)
     idx = synth.uniform_topk(rng, 2, 8, 2)
