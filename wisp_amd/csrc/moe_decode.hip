@@ -378,9 +378,25 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
             one_token_list(e, w);
             return;
         }
-        if (n_experts <= 256 && top_k <= 16) {
+        if (n_experts <= 64) {
+            /* few experts, 2-4 tokens: wave t selects token t alone, no
+             * barrier (the four-wave grouped selection ranks 64-key blocks
+             * that would be mostly empty) */
+            if (wv < M) {
+                int e;
+                float w;
+                topk_wave_small(s_sc + wv * n_experts,
+                                R.kind == WISP_ROUTER_SIGMOID ? R.bias : nullptr,
+                                R.logits + (size_t)wv * n_experts, s_ck + wv * 64, s_sel[wv],
+                                n_experts, top_k, R.kind, e, w);
+                if (lane < top_k) {
+                    s_e[wv * top_k + lane] = e;
+                    s_w[wv * top_k + lane] = w;
+                }
+            }
+        } else if (n_experts <= 256 && top_k <= 16) {
             /* up to 256 experts: two-level selection by groups of four
-             * waves, two tokens per pass, one barrier per pass */
+             * waves, two tokens per group, one barrier */
             const int grp = wv >> 2;
             const int ka = prep_key_slots(n_experts);
             if (M == 1) {
