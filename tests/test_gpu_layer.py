@@ -181,12 +181,13 @@ def test_one_token_selection_expert_counts(n_exp, k, kind):
               use_bias=(kind == "sigmoid"), repeat=2, vary_x=True)
 
 
-@pytest.mark.parametrize("n_exp", [32, 256])
-def test_sigmoid_nan_logit_never_selected(n_exp):
+@pytest.mark.parametrize("n_exp,M", [(32, 1), (256, 1), (40, 3), (256, 4)])
+def test_sigmoid_nan_logit_never_selected(n_exp, M):
     # a NaN router row gives a NaN key: the oracle's "largest untaken" never
-    # picks it, and neither may the device (one-wave and workgroup selection)
-    print(f"layer sigmoid NaN row E={n_exp}", flush=True)
-    run_layer(720 + n_exp, 256, 512, n_exp, 4, 1, "sigmoid", shared=False, use_bias=True,
+    # picks it, and neither may the device (one-wave selection per token,
+    # and the four-wave grouped selection)
+    print(f"layer sigmoid NaN row E={n_exp} M={M}", flush=True)
+    run_layer(720 + n_exp + M, 256, 512, n_exp, 4, M, "sigmoid", shared=False, use_bias=True,
               nan_rows=(1, 5))
 
 
