@@ -46,6 +46,7 @@
 #define PF_SCALE_LDS_MAX 40960    /* byte budget of the LDS scale (and zero) image */
 #define PF_SCALE_LDS_WIDE 65536   /* the same for the wide full-tile kernel      */
 #define PF_SCALE_PIECES 4         /* 16-byte scale pieces per lane and row tile when staged */
+#define PF_WIDE_RING 2         /* weight blocks in the ring of the wide full-tile kernel */
 #define PF_CHUNK 8                /* K blocks per straight-line pipeline chunk (when they divide K) */
 
 struct PfParams {
@@ -410,7 +411,29 @@ __global__ __launch_bounds__(64 * WV) void pf_gemm_kernel(const PfParams P, int 
         }
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
-            if constexpr (NT > 2) {
+            if constexpr (NT > 2 && R == 2) {
+                /* wide waves with a ring of two (the registers it frees):
+                 * every activation fragment of the k step, then the NT
+                 * weight fragments, then the TV x NT MFMAs */
+                h8 af[TV];
+#pragma unroll
+                for (int t = 0; t < TV; t++)
+                    af[t] = *(const h8*)(abuf + (16 * t + col) * PF_AROW + 32 * j + 8 * kk);
+                h8 bf[NT];
+#pragma unroll
+                for (int s = 0; s < NT; s++) {
+                    const f16 sc = __builtin_bit_cast(f16, sr[r][s]);
+                    const f16 zc = HZ ? __builtin_bit_cast(f16, zr[r][s]) : (f16)0.0f;
+                    bf[s] = dequant8<HZ>(wr[r][s][kk], (h2){sc, sc}, (h2){zc, zc},
+                                         nib_mask, nib_one);
+                }
+#pragma unroll
+                for (int t = 0; t < TV; t++)
+#pragma unroll
+                    for (int s = 0; s < NT; s++)
+                        acc[t][s] = mfma16x16x32(af[t], bf[s], acc[t][s]);
+                __builtin_amdgcn_sched_barrier(0);
+            } else if constexpr (NT > 2) {
                 /* wide waves: the NT weight fragments first, then one
                  * activation fragment at a time (registers) */
                 h8 bf[NT];
@@ -678,7 +701,8 @@ static void pf_launch_one(const PfParams& P, int gx, int cls, size_t budget, hip
 }
 
 /* The full 128-token tiles without zero points: 4 row tiles per wave
- * (256 h features or 512 output rows per workgroup, ring of 3), so each
+ * (256 h features or 512 output rows per workgroup, ring of 2: measured
+ * 1 % faster on the DeepSeek-V3 2048-token layer than a ring of 3), so each
  * activation fragment read from LDS feeds 4 MFMAs instead of 2; it fits
  * 256 VGPRs only with the scales in LDS and no zeros. Returns false when
  * the shape or the scale image does not allow it. */
@@ -695,8 +719,8 @@ static bool pf_launch_wide(const PfParams& P, int gx, hipStream_t s) {
             lds > PF_SCALE_LDS_WIDE || 2 * G > 64 * PF_SCALE_PIECES)
             return false;
         auto k = (K / 128) % PF_CHUNK == 0
-                     ? pf_gemm_kernel<GATEUP, false, 8, 3, PF_WAVES, true, NTW, PF_CHUNK>
-                     : pf_gemm_kernel<GATEUP, false, 8, 3, PF_WAVES, true, NTW>;
+                     ? pf_gemm_kernel<GATEUP, false, 8, PF_WIDE_RING, PF_WAVES, true, NTW, PF_CHUNK>
+                     : pf_gemm_kernel<GATEUP, false, 8, PF_WIDE_RING, PF_WAVES, true, NTW>;
         if (lds > 65536)
             (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
                                       (int)lds);
