@@ -47,6 +47,7 @@
 #define PF_SCALE_LDS_WIDE 65536   /* the same for the wide full-tile kernel      */
 #define PF_SCALE_PIECES 4         /* 16-byte scale pieces per lane and row tile when staged */
 #define PF_WIDE_RING 2         /* weight blocks in the ring of the wide full-tile kernel */
+#define PF_SMALL_CHUNK_DN 16      /* down K chunk of the <= 64-token tiles (all 16 blocks of inter 2048) */
 #define PF_CHUNK 8                /* K blocks per straight-line pipeline chunk (when they divide K) */
 
 struct PfParams {
@@ -688,8 +689,14 @@ static void pf_launch_one(const PfParams& P, int gx, int cls, size_t budget, hip
     const size_t lds = (size_t)WV * NT * 16 * G * 2 * (HZ ? 2 : 1);
     const int ny = GATEUP ? P.inter / (8 * NT * WV) : P.hidden / (16 * NT * WV);
     if (lds <= budget && 2 * G <= 64 * PF_SCALE_PIECES) {
-        auto k = (K / 128) % PF_CHUNK == 0 ? pf_gemm_kernel<GATEUP, HZ, TV, R, WV, true, NT, PF_CHUNK>
-                                          : pf_gemm_kernel<GATEUP, HZ, TV, R, WV, true, NT>;
+        /* the small tiles' down K loop in one straight-line chunk when it
+         * divides (no pipeline refill at chunk edges: 2.75 -> 2.74 ms;
+         * their gate/up loop in 28- or 56-block chunks needed more
+         * registers and was no faster or slower) */
+        constexpr int CS = TV <= 4 && !GATEUP ? PF_SMALL_CHUNK_DN : PF_CHUNK;
+        auto k = (K / 128) % CS == 0 ? pf_gemm_kernel<GATEUP, HZ, TV, R, WV, true, NT, CS>
+                 : (K / 128) % PF_CHUNK == 0 ? pf_gemm_kernel<GATEUP, HZ, TV, R, WV, true, NT, PF_CHUNK>
+                                            : pf_gemm_kernel<GATEUP, HZ, TV, R, WV, true, NT>;
         if (lds > 65536)
             (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
                                       (int)lds);
