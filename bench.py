@@ -252,11 +252,14 @@ def measure(layer, steps, warmup, replays):
 # ---------------------------------------------------------------------------
 
 def _cpu_info():
-    model, phys = "unknown", set()
+    model, phys, ids = "unknown", set(), {}
     try:
         with open("/proc/cpuinfo") as f:
             pid = core = None
             for ln in f:
+                key = ln.split(":", 1)[0].strip()
+                if key in ("cpu family", "model", "stepping") and key not in ids:
+                    ids[key] = ln.split(":", 1)[1].strip()
                 if ln.startswith("model name") and model == "unknown":
                     model = ln.split(":", 1)[1].strip()
                 elif ln.startswith("physical id"):
@@ -270,7 +273,10 @@ def _cpu_info():
         aff = len(os.sched_getaffinity(0))
     except AttributeError:
         aff = os.cpu_count()
-    return {"cpu": model, "logical_cpus_visible": os.cpu_count(), "cpus_in_affinity": aff,
+    # family/model/stepping identify the part when the model name is generic
+    return {"cpu": model, "cpu_family_model_stepping": "/".join(
+                ids.get(k, "?") for k in ("cpu family", "model", "stepping")),
+            "logical_cpus_visible": os.cpu_count(), "cpus_in_affinity": aff,
             "physical_cores_visible": len(phys) or None,
             "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
 
