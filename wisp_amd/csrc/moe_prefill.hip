@@ -35,6 +35,8 @@
  */
 #include "hip_common.h"
 
+#include <mutex>
+
 #define PF_BM 128                 /* tokens per tile                         */
 #define PF_WAVES 8                /* waves per workgroup (NT = 2 row tiles each) */
 #define PF_RING 4                 /* weight blocks in the register ring (3 in flight) */
@@ -742,13 +744,52 @@ static bool pf_launch_wide(const PfParams& P, int gx, hipStream_t s) {
  * a workgroup per CU and were slower, as were 4-wave workgroups with
  * accumulators in AGPRs for the full tiles). */
 template <bool GATEUP, bool HZ>
-static void pf_launch(const PfParams& P, const int* gx, hipStream_t s) {
+static void pf_launch_full(const PfParams& P, const int* gx, hipStream_t s) {
     if (!pf_launch_wide<GATEUP, HZ>(P, gx[2], s))
         pf_launch_one<GATEUP, HZ, 8, PF_RING, PF_WAVES, PF_NT>(P, gx[2], 2, PF_SCALE_LDS_MAX, s);
+}
+template <bool GATEUP, bool HZ>
+static void pf_launch_small(const PfParams& P, const int* gx, hipStream_t s) {
     pf_launch_one<GATEUP, HZ, 4, PF_RING, PF_WAVES, PF_NT>(P, gx[1], 1, PF_SCALE_LDS_MAX, s);
     /* ring of 3 for the <= 32-token tiles: 79 VGPRs, 6 waves per SIMD (3
      * workgroups per CU instead of 2), 1.5 % faster layer */
     pf_launch_one<GATEUP, HZ, 2, 3, PF_WAVES, PF_NT>(P, gx[0], 0, PF_SCALE_LDS_MAX, s);
+}
+
+/* A second stream per device for the small tiles, with the two events of
+ * the fork and the join; created on a device's first prefill call and
+ * kept until the process ends. The full 128-token tiles are bound by the
+ * matrix cores and run one workgroup per CU (DeepSeek-V3: 536 gate/up
+ * workgroups, so the third round of 256 has 24 and leaves most CUs idle);
+ * the small tiles are bound by memory. On two streams the small tiles fill
+ * the CUs the full tiles leave free. */
+#define PF_MAX_DEVICES 64
+static hipStream_t g_pf_side[PF_MAX_DEVICES];
+static hipEvent_t g_pf_fork[PF_MAX_DEVICES], g_pf_join[PF_MAX_DEVICES];
+static std::mutex g_pf_mu;
+
+/* Called with g_pf_mu held: the caller keeps it until the join is
+ * enqueued, so calls from several host threads cannot interleave their
+ * fork and join records on the shared events. */
+static hipError_t pf_side_stream(hipStream_t* s2, hipEvent_t* fork, hipEvent_t* join) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= PF_MAX_DEVICES) return hipErrorInvalidDevice;
+    if (!g_pf_side[dev]) {
+        hipStream_t st;
+        hipEvent_t a, b;
+        if ((e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&a, hipEventDisableTiming)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&b, hipEventDisableTiming)) != hipSuccess) return e;
+        g_pf_fork[dev] = a;
+        g_pf_join[dev] = b;
+        g_pf_side[dev] = st;
+    }
+    *s2 = g_pf_side[dev];
+    *fork = g_pf_fork[dev];
+    *join = g_pf_join[dev];
+    return hipSuccess;
 }
 
 extern "C" hipError_t wisp_gpu_expert_offsets(const int* d_topk_idx, int n_tokens, int top_k,
@@ -823,14 +864,33 @@ extern "C" hipError_t wisp_gpu_moe_prefill_int4(const void* const* d_expert_tabl
         gx[k] = gx[k] < P.max_tiles ? gx[k] : P.max_tiles;
         gx[k] = (gx[k] + PF_XCDS - 1) / PF_XCDS * PF_XCDS;   /* whole dies (XCD-aware order) */
     }
+    /* small tiles (gate/up, then their down) on the side stream, full
+     * tiles on the caller's; the caller's stream waits for both before the
+     * combine. EV_PF_GATEUP / EV_PF_DOWN time the full tiles' launches. */
+    hipStream_t s2;
+    hipEvent_t fork, join;
+    std::lock_guard<std::mutex> lk(g_pf_mu);
+    e = pf_side_stream(&s2, &fork, &join);
+    if (e != hipSuccess) return e;
+    if ((e = hipEventRecord(fork, s)) != hipSuccess) return e;
+    if ((e = hipStreamWaitEvent(s2, fork, 0)) != hipSuccess) return e;
+    if (hz) {
+        pf_launch_small<true, true>(P, gx, s2);
+        pf_launch_small<false, true>(P, gx, s2);
+    } else {
+        pf_launch_small<true, false>(P, gx, s2);
+        pf_launch_small<false, false>(P, gx, s2);
+    }
+    if ((e = hipEventRecord(join, s2)) != hipSuccess) return e;
     ev_before(EV_PF_GATEUP, s);
-    if (hz) pf_launch<true, true>(P, gx, s);
-    else pf_launch<true, false>(P, gx, s);
+    if (hz) pf_launch_full<true, true>(P, gx, s);
+    else pf_launch_full<true, false>(P, gx, s);
     ev_after(EV_PF_GATEUP, s);
     ev_before(EV_PF_DOWN, s);
-    if (hz) pf_launch<false, true>(P, gx, s);
-    else pf_launch<false, false>(P, gx, s);
+    if (hz) pf_launch_full<false, true>(P, gx, s);
+    else pf_launch_full<false, false>(P, gx, s);
     ev_after(EV_PF_DOWN, s);
+    if ((e = hipStreamWaitEvent(s, join, 0)) != hipSuccess) return e;
     const size_t n_out = (size_t)n_tokens * (P.hidden / 8);
     hipLaunchKernelGGL(pf_combine_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, s,
                        P);
