@@ -191,3 +191,49 @@ def test_invalid_arguments_are_rejected():
         moe.moe_prefill_int4(d.ptr, 0, L, d.ptr, 4, d.ptr, d.ptr, 2, 8, DeviceBuffer(64), d.ptr)
     with pytest.raises(Exception):
         moe.moe_prefill_int4(d.ptr, 0, L, d.ptr + 2, 4, d.ptr, d.ptr, 2, 8, ws, d.ptr)
+
+
+def test_graph_replays_match_eager():
+    """The prefill forks its small tiles onto a second stream and joins it
+    back: captured in a HIP graph on the caller's stream (after an eager
+    call), every replay gives the eager call's output bit for bit, with
+    other eager prefills and synchronisations between the replays. The
+    routing has full 128-token tiles (on the caller's stream) and small
+    tiles (on the second stream)."""
+    from wisp_amd.hip import Graph, Stream
+    print("prefill graph replays vs eager", flush=True)
+    seed, inter, hidden, gs, n_exp, k = 91, 256, 512, 128, 16, 4
+    rng = np.random.default_rng(seed)
+    idx = skewed_routing(rng, n_exp, k)
+    w = synth.route_weights(rng, idx.shape[0], k)
+    T = idx.shape[0]
+    arena = moe.ExpertArena(n_exp, inter, hidden, gs,
+                            lambda e, out: make_expert(seed, e, inter, hidden, gs, False, out),
+                            has_zeros=False)
+    sh_blob = make_expert(seed, 10_000, inter, hidden, gs, False)
+    sh_dev = DeviceBuffer(sh_blob.nbytes + 16)
+    sh_dev.upload(sh_blob, offset=8)
+    xs = [to_device(synth.make_x(rng, T, hidden)) for _ in range(2)]
+    di, dw = to_device(idx.astype(np.int32)), to_device(w.astype(np.float32))
+    ws = [DeviceBuffer(moe.prefill_workspace_bytes(arena.layout, T, k, n_exp, True))
+          for _ in range(2)]
+    outs = [DeviceBuffer(4 * T * hidden) for _ in range(2)]
+    st = Stream()
+
+    def call(i):
+        moe.moe_prefill_int4(arena.table.ptr, sh_dev.ptr + 8, arena.layout, xs[i].ptr, T,
+                             di.ptr, dw.ptr, k, n_exp, ws[i], outs[i].ptr, stream=st.handle)
+
+    call(0)
+    synchronize()
+    ref = outs[0].download(np.float32, (T, hidden))
+    graph = Graph(st, lambda: call(0))
+    for r in range(3):
+        outs[0].zero()
+        call(1)                       # other eager work on the same stream
+        synchronize()
+        graph.launch(st)
+        synchronize()
+        got = outs[0].download(np.float32, (T, hidden))
+        assert np.array_equal(got, ref), f"replay {r} differs from the eager call"
+    del graph
