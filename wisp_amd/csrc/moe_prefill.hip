@@ -768,6 +768,13 @@ static hipStream_t g_pf_side[PF_MAX_DEVICES];
 static hipEvent_t g_pf_fork[PF_MAX_DEVICES], g_pf_join[PF_MAX_DEVICES];
 static std::mutex g_pf_mu;
 
+/* True when this device's second stream exists (called with g_pf_mu held). */
+static bool pf_side_ready() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= PF_MAX_DEVICES) return false;
+    return g_pf_side[dev] != nullptr;
+}
+
 /* Called with g_pf_mu held: the caller keeps it until the join is
  * enqueued, so calls from several host threads cannot interleave their
  * fork and join records on the shared events. */
@@ -867,13 +874,27 @@ extern "C" hipError_t wisp_gpu_moe_prefill_int4(const void* const* d_expert_tabl
     /* small tiles (gate/up, then their down) on the side stream, full
      * tiles on the caller's; the caller's stream waits for both before the
      * combine. EV_PF_GATEUP / EV_PF_DOWN time the full tiles' launches. */
-    hipStream_t s2;
-    hipEvent_t fork, join;
+    hipStream_t s2 = s;
+    hipEvent_t fork = nullptr, join = nullptr;
     std::lock_guard<std::mutex> lk(g_pf_mu);
-    e = pf_side_stream(&s2, &fork, &join);
-    if (e != hipSuccess) return e;
-    if ((e = hipEventRecord(fork, s)) != hipSuccess) return e;
-    if ((e = hipStreamWaitEvent(s2, fork, 0)) != hipSuccess) return e;
+    if (pf_side_ready()) {
+        e = pf_side_stream(&s2, &fork, &join);
+        if (e != hipSuccess) return e;
+    } else {
+        /* no second stream yet and the caller's stream is being captured:
+         * create none inside the capture, run every class on the caller's
+         * stream (the next call made outside a capture creates it) */
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if ((e = hipStreamIsCapturing(s, &cs)) != hipSuccess) return e;
+        if (cs == hipStreamCaptureStatusNone) {
+            e = pf_side_stream(&s2, &fork, &join);
+            if (e != hipSuccess) return e;
+        }
+    }
+    if (fork) {
+        if ((e = hipEventRecord(fork, s)) != hipSuccess) return e;
+        if ((e = hipStreamWaitEvent(s2, fork, 0)) != hipSuccess) return e;
+    }
     if (hz) {
         pf_launch_small<true, true>(P, gx, s2);
         pf_launch_small<false, true>(P, gx, s2);
@@ -881,7 +902,7 @@ extern "C" hipError_t wisp_gpu_moe_prefill_int4(const void* const* d_expert_tabl
         pf_launch_small<true, false>(P, gx, s2);
         pf_launch_small<false, false>(P, gx, s2);
     }
-    if ((e = hipEventRecord(join, s2)) != hipSuccess) return e;
+    if (join && (e = hipEventRecord(join, s2)) != hipSuccess) return e;
     ev_before(EV_PF_GATEUP, s);
     if (hz) pf_launch_full<true, true>(P, gx, s);
     else pf_launch_full<true, false>(P, gx, s);
@@ -890,7 +911,7 @@ extern "C" hipError_t wisp_gpu_moe_prefill_int4(const void* const* d_expert_tabl
     if (hz) pf_launch_full<false, true>(P, gx, s);
     else pf_launch_full<false, false>(P, gx, s);
     ev_after(EV_PF_DOWN, s);
-    if ((e = hipStreamWaitEvent(s, join, 0)) != hipSuccess) return e;
+    if (join && (e = hipStreamWaitEvent(s, join, 0)) != hipSuccess) return e;
     const size_t n_out = (size_t)n_tokens * (P.hidden / 8);
     hipLaunchKernelGGL(pf_combine_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, s,
                        P);
