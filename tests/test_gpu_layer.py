@@ -237,3 +237,59 @@ def test_nothing_routed_writes_zeros():
                         out32.ptr, 0, accumulate=True)
     synchronize()
     assert np.array_equal(out32.download(np.float32, (M, hidden)), base)
+
+
+@pytest.mark.parametrize("hidden,M", [(7168, 4), (1024, 3)])
+def test_decode_graph_replays_match_eager(hidden, M):
+    """Captured in a HIP graph on the caller's stream (after an eager
+    call), every replay of a 3- or 4-token layer decode gives the eager
+    call's routing and output bit for bit, with other eager calls and
+    synchronisations between the replays: the per-call counters are reset
+    by kernels inside the graph, and the routing epoch carried in the
+    workspace advances on every replay. hidden 7168 takes the K-split
+    gate/up with its finishing kernel; 1024 the unsplit one."""
+    from wisp_amd.hip import Graph, Stream
+    print(f"decode graph replays vs eager: hidden={hidden} M={M}", flush=True)
+    seed, inter, n_exp, top_k = 53 + M, 256, 32, 8
+    rng = np.random.default_rng(seed)
+    blobs = [make_expert(seed, e, inter, hidden, 128) for e in range(n_exp)]
+    arena = moe.ExpertArena(n_exp, inter, hidden, 128, lambda e, out: blobs[e], has_zeros=False)
+    sb = make_expert(seed, 999, inter, hidden, 128)
+    sh = DeviceBuffer(sb.nbytes + 16)
+    sh.upload(sb, offset=8)
+    dW = to_device(synth.make_router(rng, n_exp, hidden, std=0.05))
+    xs = [to_device(synth.make_x(rng, M, hidden)) for _ in range(2)]
+    bufs = [dict(scores=DeviceBuffer(4 * M * n_exp), idx=DeviceBuffer(4 * M * top_k),
+                 w=DeviceBuffer(4 * M * top_k), out=DeviceBuffer(4 * M * hidden),
+                 ws=DeviceBuffer(moe.decode_workspace_bytes(arena.layout, M, top_k, True)))
+            for _ in range(2)]
+    st = Stream()
+
+    def call(i):
+        b = bufs[i]
+        moe.moe_layer_decode_int4(dW.ptr, 0, moe.ROUTER_SIGMOID, b["scores"].ptr, b["idx"].ptr,
+                                  b["w"].ptr, arena.table.ptr, sh.ptr + 8, arena.layout,
+                                  xs[i].ptr, M, top_k, n_exp, b["ws"], out32=b["out"].ptr,
+                                  stream=st.handle)
+
+    def read(i):
+        return (bufs[i]["idx"].download(np.int32, (M, top_k)),
+                bufs[i]["out"].download(np.float32, (M, hidden)))
+
+    call(0)
+    synchronize()
+    ref = read(0)
+    assert np.isfinite(ref[1]).all() and np.abs(ref[1]).max() > 0
+    graph = Graph(st, lambda: call(0))
+    for r in range(3):
+        bufs[0]["out"].zero()
+        call(1)                       # other eager work on the same stream
+        synchronize()
+        graph.launch(st)
+        synchronize()
+        got = read(0)
+        assert np.array_equal(got[0], ref[0]), f"replay {r}: routing differs"
+        assert np.array_equal(got[1], ref[1]), f"replay {r}: output differs from the eager call"
+    del graph
+    for b in bufs:
+        assert moe.decode_status(b["ws"]) == 0

@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/wisp_amd.h"
 
 typedef _Float16 f16;
@@ -115,5 +117,23 @@ static inline void ev_after(int i, hipStream_t s) {
     if (wisp_amd__events && i < wisp_amd__event_pairs)
         (void)hipEventRecord(wisp_amd__events[2 * i + 1], s);
 }
+
+/* ---- the library's second stream ---------------------------------------
+ * One per device, with two events (timing off) for a fork from and a join
+ * back to the caller's stream; created by the first call that asks for it
+ * outside a graph capture and kept until the process ends (the prefill
+ * runs its small tiles there). A caller takes wisp_amd__side_mu before
+ * wisp_amd__side() and keeps it until its join is enqueued, so calls from
+ * several host threads cannot interleave their records on the shared
+ * events. */
+struct SideStream {
+    hipStream_t s2;
+    hipEvent_t fork, join;
+};
+extern std::mutex wisp_amd__side_mu;
+/* With wisp_amd__side_mu held: the second stream of the device of `s` in
+ * *out, or out->s2 == nullptr when it does not exist yet and `s` is being
+ * captured (no stream is created inside a capture). */
+hipError_t wisp_amd__side(hipStream_t s, SideStream* out);
 
 static inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }

@@ -756,46 +756,37 @@ static void pf_launch_small(const PfParams& P, const int* gx, hipStream_t s) {
     pf_launch_one<GATEUP, HZ, 2, 3, PF_WAVES, PF_NT>(P, gx[0], 0, PF_SCALE_LDS_MAX, s);
 }
 
-/* A second stream per device for the small tiles, with the two events of
- * the fork and the join; created on a device's first prefill call and
- * kept until the process ends. The full 128-token tiles are bound by the
- * matrix cores and run one workgroup per CU (DeepSeek-V3: 536 gate/up
- * workgroups, so the third round of 256 has 24 and leaves most CUs idle);
- * the small tiles are bound by memory. On two streams the small tiles fill
- * the CUs the full tiles leave free. */
-#define PF_MAX_DEVICES 64
-static hipStream_t g_pf_side[PF_MAX_DEVICES];
-static hipEvent_t g_pf_fork[PF_MAX_DEVICES], g_pf_join[PF_MAX_DEVICES];
-static std::mutex g_pf_mu;
+/* The library's second stream (declared in hip_common.h). Prefill runs
+ * its small tiles there: the full 128-token tiles are bound by the matrix
+ * cores and run one workgroup per CU (DeepSeek-V3: 536 gate/up workgroups,
+ * so the third round of 256 has 24 and leaves most CUs idle); the small
+ * tiles are bound by memory and fill the CUs the full tiles leave free. */
+#define SIDE_MAX_DEVICES 64
+std::mutex wisp_amd__side_mu;
+static SideStream g_side[SIDE_MAX_DEVICES];
 
-/* True when this device's second stream exists (called with g_pf_mu held). */
-static bool pf_side_ready() {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= PF_MAX_DEVICES) return false;
-    return g_pf_side[dev] != nullptr;
-}
-
-/* Called with g_pf_mu held: the caller keeps it until the join is
- * enqueued, so calls from several host threads cannot interleave their
- * fork and join records on the shared events. */
-static hipError_t pf_side_stream(hipStream_t* s2, hipEvent_t* fork, hipEvent_t* join) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
+hipError_t wisp_amd__side(hipStream_t s, SideStream* out) {
+    *out = SideStream{nullptr, nullptr, nullptr};
+    int dev = 0, cur = 0;
+    hipError_t e = hipGetDevice(&cur);
     if (e != hipSuccess) return e;
-    if (dev < 0 || dev >= PF_MAX_DEVICES) return hipErrorInvalidDevice;
-    if (!g_pf_side[dev]) {
-        hipStream_t st;
-        hipEvent_t a, b;
-        if ((e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking)) != hipSuccess) return e;
-        if ((e = hipEventCreateWithFlags(&a, hipEventDisableTiming)) != hipSuccess) return e;
-        if ((e = hipEventCreateWithFlags(&b, hipEventDisableTiming)) != hipSuccess) return e;
-        g_pf_fork[dev] = a;
-        g_pf_join[dev] = b;
-        g_pf_side[dev] = st;
+    dev = s ? hipGetStreamDeviceId(s) : cur;
+    if (dev < 0) return hipErrorInvalidResourceHandle;
+    if (dev >= SIDE_MAX_DEVICES) return hipErrorInvalidDevice;
+    if (!g_side[dev].s2) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if ((e = hipStreamIsCapturing(s, &cs)) != hipSuccess) return e;
+        if (cs != hipStreamCaptureStatusNone) return hipSuccess;
+        if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
+        SideStream n{nullptr, nullptr, nullptr};
+        e = hipStreamCreateWithFlags(&n.s2, hipStreamNonBlocking);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&n.fork, hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&n.join, hipEventDisableTiming);
+        if (cur != dev) (void)hipSetDevice(cur);
+        if (e != hipSuccess) return e;
+        g_side[dev] = n;
     }
-    *s2 = g_pf_side[dev];
-    *fork = g_pf_fork[dev];
-    *join = g_pf_join[dev];
+    *out = g_side[dev];
     return hipSuccess;
 }
 
@@ -874,23 +865,14 @@ extern "C" hipError_t wisp_gpu_moe_prefill_int4(const void* const* d_expert_tabl
     /* small tiles (gate/up, then their down) on the side stream, full
      * tiles on the caller's; the caller's stream waits for both before the
      * combine. EV_PF_GATEUP / EV_PF_DOWN time the full tiles' launches. */
-    hipStream_t s2 = s;
-    hipEvent_t fork = nullptr, join = nullptr;
-    std::lock_guard<std::mutex> lk(g_pf_mu);
-    if (pf_side_ready()) {
-        e = pf_side_stream(&s2, &fork, &join);
-        if (e != hipSuccess) return e;
-    } else {
-        /* no second stream yet and the caller's stream is being captured:
-         * create none inside the capture, run every class on the caller's
-         * stream (the next call made outside a capture creates it) */
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if ((e = hipStreamIsCapturing(s, &cs)) != hipSuccess) return e;
-        if (cs == hipStreamCaptureStatusNone) {
-            e = pf_side_stream(&s2, &fork, &join);
-            if (e != hipSuccess) return e;
-        }
-    }
+    SideStream side;
+    std::lock_guard<std::mutex> lk(wisp_amd__side_mu);
+    if ((e = wisp_amd__side(s, &side)) != hipSuccess) return e;
+    /* no second stream yet and the caller's stream is being captured:
+     * every class runs on the caller's stream (the next call made outside
+     * a capture creates it) */
+    hipStream_t s2 = side.s2 ? side.s2 : s;
+    const hipEvent_t fork = side.fork, join = side.join;
     if (fork) {
         if ((e = hipEventRecord(fork, s)) != hipSuccess) return e;
         if ((e = hipStreamWaitEvent(s2, fork, 0)) != hipSuccess) return e;
