@@ -51,6 +51,7 @@
 #define PF_WIDE_RING 2         /* weight blocks in the ring of the wide full-tile kernel */
 #define PF_SMALL_CHUNK_DN 16      /* down K chunk of the <= 64-token tiles (all 16 blocks of inter 2048) */
 #define PF_CHUNK 8                /* K blocks per straight-line pipeline chunk (when they divide K) */
+#define PF_WIDE_CHUNK_DN 16       /* down K chunk of the wide full-tile kernel (all 16 blocks of inter 2048) */
 
 struct PfParams {
     uint64_t p_off[3], s_off[3], z_off[3];
@@ -727,8 +728,11 @@ static bool pf_launch_wide(const PfParams& P, int gx, hipStream_t s) {
         if (P.inter % (8 * NTW * PF_WAVES) || P.hidden % (16 * NTW * PF_WAVES) ||
             lds > PF_SCALE_LDS_WIDE || 2 * G > 64 * PF_SCALE_PIECES)
             return false;
-        auto k = (K / 128) % PF_CHUNK == 0
-                     ? pf_gemm_kernel<GATEUP, false, 8, PF_WIDE_RING, PF_WAVES, true, NTW, PF_CHUNK>
+        /* down in one chunk when it divides (2.672 -> 2.666 ms; the gate/up
+         * loop in chunks of 14 or 28 blocks spilled and was slower) */
+        constexpr int WC = GATEUP ? PF_CHUNK : PF_WIDE_CHUNK_DN;
+        auto k = (K / 128) % WC == 0
+                     ? pf_gemm_kernel<GATEUP, false, 8, PF_WIDE_RING, PF_WAVES, true, NTW, WC>
                      : pf_gemm_kernel<GATEUP, false, 8, PF_WIDE_RING, PF_WAVES, true, NTW>;
         if (lds > 65536)
             (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -757,10 +761,10 @@ static void pf_launch_small(const PfParams& P, const int* gx, hipStream_t s) {
 }
 
 /* The library's second stream (declared in hip_common.h). Prefill runs
- * its small tiles there: the full 128-token tiles are bound by the matrix
- * cores and run one workgroup per CU (DeepSeek-V3: 536 gate/up workgroups,
- * so the third round of 256 has 24 and leaves most CUs idle); the small
- * tiles are bound by memory and fill the CUs the full tiles leave free. */
+ * its small tiles there: the tiles of 65-128 tokens are bound by the matrix
+ * cores and run one workgroup per CU (DeepSeek-V3, 2048 tokens: 928 gate/up
+ * workgroups, so the fourth round of 256 has 160 and leaves CUs idle); the
+ * small tiles are bound by memory and fill the CUs the others leave free. */
 #define SIDE_MAX_DEVICES 64
 std::mutex wisp_amd__side_mu;
 static SideStream g_side[SIDE_MAX_DEVICES];
