@@ -25,8 +25,8 @@ def cosine(got, want):
     return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-300))
 
 
-# Parity bar for fp16 outputs: max |err| / max |ref|
-# <= 1e-2 and cosine >= 0.9999 against the CPU oracle.
+# Parity bar for fp16 outputs: max |err| / max |ref| <= 1e-2 and cosine
+# >= 0.9999 against the CPU oracle.
 MAX_REL = 1e-2
 MIN_COS = 0.9999
 
