@@ -49,7 +49,8 @@ def test_float_to_half_rne_vs_numpy():
         np.array([0.0, -0.0, 65504.0, 65520.0, 65519.99, 6.1e-5, 5.96e-8, 2.98e-8, 2.99e-8,
                   1e-9, -1e-9, np.inf, -np.inf, 1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11], np.float32),
     ]).astype(np.float32)
-    want = vals.astype(np.float16).view(np.uint16)
+    with np.errstate(over="ignore"):   # values past 65519.99 round to inf on purpose
+        want = vals.astype(np.float16).view(np.uint16)
     got = np.array([o.orc_float_to_half(float(v)) for v in vals], dtype=np.uint16)
     assert np.array_equal(got, want)
 
