@@ -237,3 +237,69 @@ def test_graph_replays_match_eager():
         got = outs[0].download(np.float32, (T, hidden))
         assert np.array_equal(got, ref), f"replay {r} differs from the eager call"
     del graph
+
+
+def test_concurrent_host_threads_match_serial():
+    """Two host threads enqueue prefills at the same time, each on its own
+    stream with its own workspace and output, while the library's second
+    stream (one per device, with shared fork and join events) serves both:
+    every output equals the one computed by a single thread, bit for bit."""
+    import threading
+
+    from wisp_amd.hip import Stream
+    print("prefill from two host threads vs serial", flush=True)
+    seed, inter, hidden, gs, n_exp, k = 97, 256, 512, 128, 16, 4
+    rng = np.random.default_rng(seed)
+    idx = skewed_routing(rng, n_exp, k)
+    w = synth.route_weights(rng, idx.shape[0], k)
+    T = idx.shape[0]
+    arena = moe.ExpertArena(n_exp, inter, hidden, gs,
+                            lambda e, out: make_expert(seed, e, inter, hidden, gs, False, out),
+                            has_zeros=False)
+    sh_blob = make_expert(seed, 20_000, inter, hidden, gs, False)
+    sh_dev = DeviceBuffer(sh_blob.nbytes + 16)
+    sh_dev.upload(sh_blob, offset=8)
+    di, dw = to_device(idx.astype(np.int32)), to_device(w.astype(np.float32))
+    n_thr, reps = 2, 6
+    xs = [to_device(synth.make_x(rng, T, hidden)) for _ in range(n_thr)]
+    ws = [DeviceBuffer(moe.prefill_workspace_bytes(arena.layout, T, k, n_exp, True))
+          for _ in range(n_thr)]
+    outs = [[DeviceBuffer(4 * T * hidden) for _ in range(reps)] for _ in range(n_thr)]
+    streams = [Stream() for _ in range(n_thr)]
+
+    def call(i, r):
+        moe.moe_prefill_int4(arena.table.ptr, sh_dev.ptr + 8, arena.layout, xs[i].ptr, T,
+                             di.ptr, dw.ptr, k, n_exp, ws[i], outs[i][r].ptr,
+                             stream=streams[i].handle)
+
+    ref = []
+    for i in range(n_thr):
+        call(i, 0)
+        streams[i].synchronize()
+        ref.append(outs[i][0].download(np.float32, (T, hidden)))
+    assert not np.array_equal(ref[0], ref[1])
+    errors = []
+
+    def worker(i):
+        try:
+            for r in range(reps):
+                call(i, r)
+            streams[i].synchronize()
+        except Exception as ex:  # reported below, in the main thread
+            errors.append(ex)
+
+    for o in outs:
+        for b in o:
+            b.zero()
+    synchronize()
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(n_thr)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    synchronize()
+    for i in range(n_thr):
+        for r in range(reps):
+            got = outs[i][r].download(np.float32, (T, hidden))
+            assert np.array_equal(got, ref[i]), f"thread {i} call {r} differs from the serial call"
