@@ -1299,26 +1299,37 @@ void down_kernel(const DecodeParams P) {
 }
 
 /* After the separate down launch: out[v][r] = the sum of part[unit][v][r]
- * over the call's wave units, in unit order from zero. One thread per
- * output. */
+ * over the call's wave units. Four lanes per output: lane k adds the units
+ * [k Q, k Q + Q) in unit order (Q = ceil(units / 4)), all its loads in
+ * flight at once for up to 4 DEC_COMBINE_BATCH units, then the first lane
+ * adds the four partial sums in lane order, so every call sums in the same
+ * order. */
+#define DEC_COMBINE_LANES 4
+#define DEC_COMBINE_BATCH 32
 template <int M>
 __global__ __launch_bounds__(256) void down_combine_kernel(const DecodeParams P) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= M * P.hidden) return;
+    const int g = blockIdx.x * 256 + threadIdx.x;
+    const int i = g / DEC_COMBINE_LANES, k = g % DEC_COMBINE_LANES;
+    const bool live = i < M * P.hidden;
     const int n_units = *P.n_unique * P.upe;
-    const float* src = P.part + i;
+    const int qn = (n_units + DEC_COMBINE_LANES - 1) / DEC_COMBINE_LANES;
+    const int q_lo = k * qn, q_hi = min(q_lo + qn, n_units);
+    const float* src = P.part + (live ? i : 0);
     const size_t stride = (size_t)M * P.hidden;
-    constexpr int MAXQ = 32;
     float y = 0.0f;
-    for (int q0 = 0; q0 < n_units; q0 += MAXQ) {
-        float t[MAXQ];
+    for (int q0 = q_lo; q0 < q_hi; q0 += DEC_COMBINE_BATCH) {
+        float t[DEC_COMBINE_BATCH];
 #pragma unroll
-        for (int qq = 0; qq < MAXQ; qq++)
-            t[qq] = q0 + qq < n_units ? src[(size_t)(q0 + qq) * stride] : 0.0f;
+        for (int qq = 0; qq < DEC_COMBINE_BATCH; qq++)
+            t[qq] = q0 + qq < q_hi ? src[(size_t)(q0 + qq) * stride] : 0.0f;
 #pragma unroll
-        for (int qq = 0; qq < MAXQ; qq++) y += t[qq];
+        for (int qq = 0; qq < DEC_COMBINE_BATCH; qq++) y += t[qq];
     }
-    store_out(P, i, y);
+    /* every lane takes part in the shuffles (no return before them) */
+    float tot = __shfl(y, 0, DEC_COMBINE_LANES);
+#pragma unroll
+    for (int q = 1; q < DEC_COMBINE_LANES; q++) tot += __shfl(y, q, DEC_COMBINE_LANES);
+    if (live && k == 0) store_out(P, i, tot);
 }
 
 /* One launch for gate/up and down: the first max_u * inter / 16 * gsplit
@@ -1473,8 +1484,8 @@ static hipError_t launch_down(const DecodeParams& P, hipStream_t s) {
     auto k = down_kernel<M, NG, HZ>;
     hipLaunchKernelGGL(k, dim3(P.hidden / (16 * DN_WAVES), P.max_u * P.upe), dim3(64 * DN_WAVES),
                        L.bytes, s, P);
-    hipLaunchKernelGGL(down_combine_kernel<M>, dim3((M * P.hidden + 255) / 256), dim3(256), 0, s,
-                       P);
+    hipLaunchKernelGGL(down_combine_kernel<M>,
+                       dim3((M * P.hidden * DEC_COMBINE_LANES + 255) / 256), dim3(256), 0, s, P);
     return hipSuccess;
 }
 
