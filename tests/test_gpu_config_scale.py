@@ -44,9 +44,9 @@ def _pick_prefill_tokens(idx):
             pick.add(toks_big[b])
     pick.update(toks_big[-2:])                                # the tail tile
     # tokens with a pair in a tile of each smaller class: remainders of
-    # <= 32, 33..64 and 65..127 tokens
+    # <= 32, 33..64, 65..96 and 97..127 tokens
     rem = counts % 128
-    for lo, hi in ((1, 32), (33, 64), (65, 127)):
+    for lo, hi in ((1, 32), (33, 64), (65, 96), (97, 127)):
         hit = [t for t in range(idx.shape[0]) if ((rem[idx[t]] >= lo) & (rem[idx[t]] <= hi)).any()]
         pick.update(hit[:3])
         pick.update(hit[-1:])

@@ -64,14 +64,19 @@ def run_prefill(seed, inter, hidden, gs, n_exp, idx, w, shared, zeros, check_tok
 
 
 def skewed_routing(rng, n_exp, k):
-    """Per-expert token counts 300, 128, 129, 1, then nothing for the rest
-    but a few spread tokens; returns idx [T, k] with distinct experts per
-    token."""
-    want = {0: 300, 1: 128, 2: 129, 3: 1}
+    """Per-expert token counts 300, 128, 129, 1, 80 (expert 4: a tile of
+    65-96 tokens) and 100 (expert 6: a tile of 97-128), then nothing for
+    the rest but a few spread tokens; returns idx [T, k] with distinct
+    experts per token."""
+    want = {0: 300, 1: 128, 2: 129, 3: 1, 4: 80, 6: 100}
     T = 320
     idx = np.full((T, k), -1, np.int32)
     fill = np.zeros(T, np.int32)
     order = rng.permutation(T)
+    # a handful of tokens also use experts 5 and 9; 7, 8 and 10+ stay empty
+    for t in order[:7]:
+        idx[t, 0] = 5 if t % 2 else 9
+        fill[t] = 1
     for e, c in want.items():
         placed = 0
         for t in order:
@@ -82,11 +87,6 @@ def skewed_routing(rng, n_exp, k):
                 fill[t] += 1
                 placed += 1
         assert placed == c
-    # a handful of tokens also use experts 5 and 9; 4, 6-8 and 10+ stay empty
-    for t in order[:7]:
-        if fill[t] < k:
-            idx[t, fill[t]] = 5 if t % 2 else 9
-            fill[t] += 1
     return idx
 
 
