@@ -39,3 +39,25 @@ def assert_close(got, want, what=""):
     r, c = rel_err(got, want), cosine(got, want)
     assert r <= MAX_REL and c >= MIN_COS, f"{what}: max-rel-err {r:.3e}, cosine {c:.7f}"
     return r, c
+
+
+def assert_valid_topk(keys, sel, k, tol, what=""):
+    """A selection decided by a near-tie of float64 `keys` (NaN or -inf:
+    never selectable) must still be a top-k within `tol`: k distinct experts
+    (or every selectable one when fewer), each no more than tol below the
+    k-th largest key, no unselected key more than tol above it, and keys
+    non-increasing in rank order within tol."""
+    keys = np.asarray(keys, np.float64)
+    ok = np.isfinite(keys)
+    sel = [int(e) for e in sel if e >= 0]
+    n_ok = int(ok.sum())
+    assert len(sel) == min(k, n_ok) and len(set(sel)) == len(sel), (what, sel)
+    assert all(ok[e] for e in sel), (what, sel)
+    if not sel:
+        return
+    kth = np.sort(keys[ok])[::-1][len(sel) - 1]
+    assert np.all(keys[sel] >= kth - tol), (what, sel, keys[sel], kth)
+    rest = np.setdiff1d(np.nonzero(ok)[0], sel)
+    if rest.size:
+        assert np.max(keys[rest]) <= kth + tol, (what, np.max(keys[rest]), kth)
+    assert np.all(np.diff(keys[sel]) <= tol), (what, keys[sel])

@@ -493,3 +493,29 @@ def test_layer_ops_closed_forms():
     xt = rng.standard_normal(40).astype(np.float32)
     want = W.astype(np.float64).T @ xt.astype(np.float64)
     assert np.max(np.abs(O.gemv_t_f16(W, xt) - want)) <= 1e-5 * np.max(np.abs(want))
+
+
+def test_valid_topk_checker_accepts_ties_and_rejects_wrong_selections():
+    """The near-tie check the GPU routing tests fall back on: it accepts any
+    order of tied keys and rejects a selection that misses a clearly larger
+    key, repeats an expert, takes a non-selectable one or is out of rank
+    order (mistakes planted here, on the CPU)."""
+    from tests.gpu_util import assert_valid_topk
+    keys = np.array([0.5, 2.0, 2.0 + 1e-9, -np.inf, 1.0, 2.0 - 1e-9, np.nan, 0.1])
+    tol = 1e-6
+    assert_valid_topk(keys, [2, 1, 5], 3, tol)        # the three tied keys, any order
+    assert_valid_topk(keys, [5, 2, 1], 3, tol)
+    assert_valid_topk(keys, [2, 1, 5, 4], 4, tol)
+    bad = [([2, 1, 4], "misses a larger key"), ([2, 2, 5], "repeats"),
+           ([2, 1, 3], "non-selectable"), ([4, 2, 1, 5], "out of rank order"),
+           ([2, 1], "too few")]
+    for sel, why in bad:
+        k = 4 if len(sel) == 4 else 3
+        with pytest.raises(AssertionError):
+            assert_valid_topk(keys, sel, k, tol)
+            print("accepted", why)
+    # fewer selectable keys than k: all of them, then -1
+    few = np.array([np.nan, 3.0, -np.inf, 1.0])
+    assert_valid_topk(few, [1, 3, -1, -1], 4, tol)
+    with pytest.raises(AssertionError):
+        assert_valid_topk(few, [1, -1, -1, -1], 4, tol)
