@@ -184,7 +184,7 @@ hipError_t wisp_gpu_topk_from_logits(const float* d_logits,
  * flat pair indices (token*top_k + slot) grouped by expert, stable in flat
  * order within an expert; inv[flat] = position of that pair in order[]
  * (-1 for pairs with an out-of-range expert id). One workgroup;
- * n_experts <= 4096. */
+ * n_experts <= 1024 (a histogram row per wave in LDS). */
 hipError_t wisp_gpu_expert_offsets(const int* d_topk_idx, int n_tokens,
                                    int top_k, int n_experts, int* d_counts,
                                    int* d_offsets, int* d_order, int* d_inv,

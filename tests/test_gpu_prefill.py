@@ -303,3 +303,35 @@ def test_concurrent_host_threads_match_serial():
         for r in range(reps):
             got = outs[i][r].download(np.float32, (T, hidden))
             assert np.array_equal(got, ref[i]), f"thread {i} call {r} differs from the serial call"
+
+
+def test_many_experts():
+    """1,023 routed experts plus the shared one, the most the prefill takes
+    (the expert-offset builder keeps a histogram row per wave in LDS): the
+    offsets and the tile list cover the top ids, with a 150-token expert
+    near the top of the range (a full tile plus a remainder) and the others
+    spread over the whole range. One more expert is rejected before any
+    launch."""
+    print("prefill 1023 experts", flush=True)
+    rng = np.random.default_rng(1023)
+    n_exp, k, T = 1023, 4, 160
+    heavy = 1000
+    idx = np.empty((T, k), np.int32)
+    for t in range(T):
+        others = rng.choice(n_exp - 1, size=k, replace=False)
+        others = np.where(others >= heavy, others + 1, others)   # never the heavy expert
+        idx[t] = others
+        if t < 150:
+            idx[t, t % k] = heavy
+    idx[0, 1 if idx[0, 0] == heavy else 0] = n_exp - 1
+    assert all(len(set(r)) == k for r in idx)
+    w = synth.route_weights(rng, T, k)
+    run_prefill(77, 256, 512, 128, n_exp, idx, w, True, False,
+                check_tokens=[0, 1, 75, 127, 128, 149, 150, T - 1])
+    L = moe.layout_from_blob(synth.make_blob(rng, 256, 512, 128), has_zeros=False)
+    assert moe.prefill_workspace_bytes(L, T, k, n_exp, True) > 0
+    assert moe.prefill_workspace_bytes(L, T, k, n_exp + 1, True) == 0
+    d = DeviceBuffer(1 << 16)
+    with pytest.raises(Exception):
+        moe.moe_prefill_int4(d.ptr, d.ptr, L, d.ptr, 4, d.ptr, d.ptr, 2, n_exp + 1,
+                             DeviceBuffer(1 << 20), d.ptr)

@@ -43,7 +43,8 @@
 #define PF_NT 2                   /* row tiles of 16 weight rows per wave        */
 #define PF_XCDS 8                 /* accelerator dies: workgroups are dealt to them round-robin */
 #define PF_AROW 136               /* LDS A row stride in halves (128 + 8)    */
-#define PF_MAX_EXPERTS 4096
+#define PF_MAX_EXPERTS 4096      /* capacity of the tile-list kernel */
+#define PF_MAX_EXPERTS1 1024      /* routed + shared experts: wisp_gpu_expert_offsets' limit */
 #define PF_CLASSES 3              /* tiles of <= 32, <= 64, <= 128 tokens    */
 #define PF_SCALE_LDS_MAX 40960    /* byte budget of the LDS scale (and zero) image */
 #define PF_SCALE_LDS_WIDE 65536   /* the same for the wide full-tile kernel      */
@@ -675,7 +676,7 @@ static bool pf_shape_ok(const WispExpertLayout* L) {
 
 extern "C" size_t wisp_moe_prefill_workspace_bytes(const WispExpertLayout* L, int n_tokens,
                                                    int top_k, int n_experts, int has_shared) {
-    if (!L || n_tokens < 1 || top_k < 1 || n_experts < 1 || n_experts + 1 > PF_MAX_EXPERTS)
+    if (!L || n_tokens < 1 || top_k < 1 || n_experts < 1 || n_experts + 1 > PF_MAX_EXPERTS1)
         return 0;
     return pf_ws_layout(L, n_tokens, top_k, n_experts, has_shared).total;
 }
@@ -806,7 +807,7 @@ extern "C" hipError_t wisp_gpu_moe_prefill_int4(const void* const* d_expert_tabl
                                                 void* d_workspace, size_t workspace_bytes,
                                                 int accumulate, float* d_out_f32,
                                                 wisp_half* d_out_f16, hipStream_t s) {
-    if (!L || n_tokens < 1 || top_k < 1 || n_experts < 1 || n_experts + 1 > PF_MAX_EXPERTS ||
+    if (!L || n_tokens < 1 || top_k < 1 || n_experts < 1 || n_experts + 1 > PF_MAX_EXPERTS1 ||
         !d_expert_table || !d_x || !d_topk_idx || !d_topk_w || !d_workspace ||
         (!d_out_f32 && !d_out_f16) || ((uintptr_t)d_x % 16) || ((uintptr_t)d_out_f32 % 16) ||
         ((uintptr_t)d_out_f16 % 16))
