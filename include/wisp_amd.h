@@ -252,7 +252,7 @@ enum {
 hipError_t wisp_moe_decode_status(void* d_workspace, hipStream_t s,
                                   uint32_t* flags, int clear);
 
-/* n_experts: 1..1024.
+/* n_experts: 1..1024; top_k: 1..64.
  * d_expert_table: device array [n_experts] of device blob base pointers
  *   (each blob base at 8 mod 16, see wisp_expert_layout_check).
  * d_shared_blob: device blob of the always-on shared expert, or NULL.
@@ -260,8 +260,9 @@ hipError_t wisp_moe_decode_status(void* d_workspace, hipStream_t s,
  * d_topk_idx / d_topk_w: [n_tokens, top_k] (device); idx < 0 is skipped.
  * d_out_f32 / d_out_f16: [n_tokens, hidden]; either may be NULL. With
  *   accumulate != 0, d_out_f32 is added to instead of overwritten.
- * Returns hipErrorInvalidValue for n_tokens outside 1..4, a layout that
- * wisp_expert_layout_check rejects, or a workspace that is too small. */
+ * Returns hipErrorInvalidValue for n_tokens outside 1..4, n_experts or
+ * top_k outside the ranges above, a layout that wisp_expert_layout_check
+ * rejects, or a workspace that is too small. */
 hipError_t wisp_gpu_moe_decode_int4(const void* const* d_expert_table,
                                     const void* d_shared_blob,
                                     const WispExpertLayout* L,

@@ -152,3 +152,8 @@ def test_invalid_arguments_are_rejected():
     small = DeviceBuffer(64)
     with pytest.raises(Exception):
         moe.moe_decode_int4(d.ptr, 0, L, d.ptr, 1, d.ptr, d.ptr, 2, 8, small, d.ptr)
+    # expert count and top-k past the documented ranges are rejected before any launch
+    big = DeviceBuffer(moe.decode_workspace_bytes(L, 1, 64, False))
+    for k, n_exp in ((65, 128), (0, 8), (2, 1025), (2, 0)):
+        with pytest.raises(Exception):
+            moe.moe_decode_int4(d.ptr, 0, L, d.ptr, 1, d.ptr, d.ptr, k, n_exp, big, d.ptr)
