@@ -621,7 +621,8 @@ extern "C" hipError_t wisp_tier_moe_decode_layer(WispExpertTier* t, int layer,
                                                  float* d_out_f32, wisp_half* d_out_f16,
                                                  hipStream_t compute) {
     if (!t || layer < 0 || layer >= t->pol.L || n_tokens < 1 || top_k < 1 || !h_topk_idx ||
-        !h_topk_w || n_tokens * top_k > WISP_TIER_MAX_PAIRS || !d_out_f32)
+        !h_topk_w || n_tokens > WISP_TIER_MAX_PAIRS || top_k > WISP_TIER_MAX_PAIRS ||
+        n_tokens * top_k > WISP_TIER_MAX_PAIRS || !d_out_f32)   /* no int overflow */
         return hipErrorInvalidValue;
     const int np = n_tokens * top_k;
     const int E = t->pol.E;
