@@ -446,6 +446,76 @@ def measure_prefill(layer, n_tokens, steps, warmup, replays):
     }
 
 
+def measure_block(layer, rows, steps, warmup, replays, per_token_us):
+    """The MoE block entry (x += MoE(RMSNorm(x) * w_norm), router on the
+    normalised rows) on `rows` drafted tokens of one speculative-verify
+    step, on the DeepSeek-V3 layer's rotating expert sets and shared/router
+    variants, with a pool of fp32 residual rows updated in place. w_norm is
+    scaled by 1e-3: the top-k of the bias-free sigmoid router does not
+    depend on the scale of its input, so the routing draws what the plain
+    layer call draws, while the MoE adds almost nothing to x, so the rows
+    (and their routing) do not drift over the timed calls. Graph replays of
+    `steps` calls, HIP events. Beside it, the reference's shape of the same
+    work: one single-token layer per drafted token (`per_token_us` each)."""
+    from wisp_amd import moe
+    from wisp_amd.hip import DeviceBuffer, Event, Graph, synchronize, to_device
+    s = layer.shape
+    rng = np.random.default_rng(4242 + rows)
+    n_pool = 16
+    x = rng.standard_normal((n_pool, rows, s.hidden)).astype(np.float32)
+    dx = to_device(x)
+    norm_w = to_device((1e-3 * (1.0 + 0.05 * rng.standard_normal(s.hidden))).astype(np.float16))
+    scores = DeviceBuffer(4 * rows * s.n_experts)
+    idx, w = DeviceBuffer(4 * rows * s.top_k), DeviceBuffer(4 * rows * s.top_k)
+    ws = DeviceBuffer(moe.block_workspace_bytes(layer.arenas[0].layout, rows, s.top_k,
+                                                s.n_experts, s.shared))
+    st = layer.stream
+
+    def step(i):
+        a = layer.arenas[i % len(layer.arenas)]
+        v = i % layer.n_var
+        moe.moe_block_int4(dx.ptr + (i % n_pool) * rows * s.hidden * 4, norm_w.ptr, 1e-6,
+                           layer.dW[v].ptr, 0, layer.kind, scores.ptr, idx.ptr, w.ptr,
+                           a.table.ptr, layer.shared_dev[v].ptr + 8 if s.shared else 0,
+                           a.layout, rows, s.top_k, s.n_experts, ws, stream=st.handle)
+
+    def unique_now():
+        ids = idx.download(np.int32, (rows, s.top_k))
+        return len({int(e) for e in ids.reshape(-1) if e >= 0}) + (1 if s.shared else 0)
+
+    n_unique = []
+    for i in range(max(warmup, n_pool)):      # eager calls; the routing each one drew
+        step(i)
+        synchronize()
+        n_unique.append(unique_now())
+    graph = Graph(st, lambda: [step(i) for i in range(steps)])
+    graph.launch(st)
+    synchronize()
+    e0, e1 = Event(), Event()
+    per = []
+    for _ in range(replays):
+        e0.record(st.handle)
+        graph.launch(st)
+        e1.record(st.handle)
+        synchronize()
+        per.append(1e3 * e0.elapsed_ms(e1) / steps)
+    del graph
+    n_after = []
+    for i in range(n_pool):                   # the same rows after the timed calls
+        step(i)
+        synchronize()
+        n_after.append(unique_now())
+    us = float(np.median(per))
+    return {"rows": rows, "us_per_call": round(us, 3), "us_min": round(float(np.min(per)), 3),
+            "n_unique_experts": round(float(np.mean(n_unique)), 2),
+            "n_unique_experts_after": round(float(np.mean(n_after)), 2),
+            "us_max": round(float(np.max(per)), 3), "replays": replays,
+            "us_per_row": round(us / rows, 3),
+            "per_token_loop_us": round(rows * per_token_us, 3),
+            "speedup_vs_per_token_loop": round(rows * per_token_us / us, 3),
+            "path": "fused decode (<= 4 rows)" if rows <= 4 else "grouped GEMM (> 4 rows)"}
+
+
 def measure_streaming(n_layers=8, steps=256, slot_frac=0.30, seed=55, n_templates=16):
     """Expert-streaming decode: n_layers DeepSeek-V3-shape MoE layers whose
     256 routed experts each live in pinned host RAM, a VRAM LRU of slot_frac
@@ -572,6 +642,8 @@ def main():
                     help="only the DeepSeek-V3 decode layer with M tokens (profiling runs)")
     ap.add_argument("--mixtral-decode-only", type=int, default=0, metavar="M",
                     help="only the Mixtral-8x7B decode layer with M tokens (profiling runs)")
+    ap.add_argument("--verify-only", type=int, default=0, metavar="ROWS",
+                    help="only the DeepSeek-V3 MoE block on ROWS drafted tokens (speculative verify)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB 5 times (byte-counter calibration)")
     args = ap.parse_args()
@@ -599,6 +671,12 @@ def main():
         mx = Layer(synth.MIXTRAL, args.mixtral_decode_only, seed=synth.MIXTRAL_BENCH_SEED, n_sets=4)
         r = measure(mx, steps, warmup, replays)
         print(json.dumps({f"mixtral-8x7b-decode-m{args.mixtral_decode_only}": r}), flush=True)
+        return
+    if args.verify_only:
+        ds = dsv3_layer(1)
+        m1 = measure(ds, steps, warmup, replays)
+        r = measure_block(ds, args.verify_only, steps, warmup, replays, m1["us_per_layer"])
+        print(json.dumps({f"deepseek-v3-verify-block-{args.verify_only}": r}), flush=True)
         return
     if args.streaming_only:
         r = measure_streaming(steps=args.stream_steps)
@@ -658,6 +736,10 @@ def main():
             key = f"deepseek-v3-decode-m{M}"
             extra[key] = measure(head, sub, 4, replays)
             log(f"{key}: {extra[key]['us_per_layer']} us, kernels {extra[key]['kernel_us']}")
+        for rows in (4, 8):
+            key = f"deepseek-v3-verify-block-{rows}"
+            extra[key] = measure_block(head, rows, sub, 4, replays, m["us_per_layer"])
+            log(f"{key}: {extra[key]}")
         extra["deepseek-v3-prefill-2048"] = measure_prefill(head, 2048, 5, 2, replays)
         log(f"deepseek-v3 prefill: {extra['deepseek-v3-prefill-2048']}")
         del head

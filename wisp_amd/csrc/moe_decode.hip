@@ -1555,12 +1555,16 @@ extern "C" void wisp_amd__test_decode_wait(int poll_limit, int extra) {
 }
 
 /* Shared body of the decode entry points: R.mode selects where the
- * routing comes from (see RouteArgs). */
+ * routing comes from (see RouteArgs). x16: an fp16 copy of an fp32 x
+ * (16-byte aligned, [M][hidden], each element the fp16 rounding of x's),
+ * made by the caller; the experts read it and the prep kernel converts
+ * nothing. */
 static hipError_t decode_run(const void* const* d_expert_table, const void* d_shared_blob,
                              const WispExpertLayout* L, const void* d_x, int x_dtype, int M,
                              RouteArgs R, int top_k, int n_experts, void* d_workspace,
                              size_t workspace_bytes, int accumulate, float* d_out_f32,
-                             wisp_half* d_out_f16, hipStream_t s) {
+                             wisp_half* d_out_f16, hipStream_t s,
+                             const uint16_t* x16 = nullptr) {
     if (wisp_expert_layout_check(L) != hipSuccess) return hipErrorInvalidValue;
     const WsLayout w = ws_layout(L, M, top_k, d_shared_blob != nullptr);
     if (workspace_bytes < w.total) return hipErrorInvalidValue;
@@ -1595,8 +1599,8 @@ static hipError_t decode_run(const void* const* d_expert_table, const void* d_sh
     P.ublob = (const uint8_t**)(ws + w.ublob);
     P.uw = (float*)(ws + w.uw);
     const bool x_direct = x_dtype == WISP_DTYPE_F16 && ((uintptr_t)d_x % 16) == 0;
-    P.xconv = x_direct ? nullptr : (uint16_t*)(ws + w.xconv);
-    P.xh = x_direct ? (const uint16_t*)d_x : P.xconv;
+    P.xconv = x_direct || x16 ? nullptr : (uint16_t*)(ws + w.xconv);
+    P.xh = x_direct ? (const uint16_t*)d_x : (x16 ? x16 : P.xconv);
     P.hperm = (uint16_t*)(ws + w.hperm);
     P.part = (float*)(ws + w.part);
     P.gsplit = fused_shape(P.hidden / 128).gsplit;
@@ -1692,7 +1696,7 @@ static hipError_t layer_run(const wisp_half* d_router_w, const wisp_half* d_rout
                             const WispExpertLayout* L, const void* d_x, int x_dtype, int n_tokens,
                             int top_k, int n_experts, void* d_workspace, size_t workspace_bytes,
                             int accumulate, float* d_out_f32, wisp_half* d_out_f16,
-                            hipStream_t s) {
+                            hipStream_t s, const uint16_t* x16 = nullptr) {
     const int hidden = (int)L->cols[0];
     /* the router GEMV runs in router workgroups of the prep launch (mode 3):
      * each thread takes at most 2 16-byte pieces of a row, so rows up to
@@ -1713,7 +1717,8 @@ static hipError_t layer_run(const wisp_half* d_router_w, const wisp_half* d_rout
         if (e != hipSuccess) return e;
     }
     return decode_run(d_expert_table, d_shared_blob, L, d_x, x_dtype, n_tokens, R, top_k,
-                      n_experts, d_workspace, workspace_bytes, accumulate, d_out_f32, d_out_f16, s);
+                      n_experts, d_workspace, workspace_bytes, accumulate, d_out_f32, d_out_f16, s,
+                      x16);
 }
 
 extern "C" hipError_t wisp_gpu_moe_layer_decode_int4(
@@ -1809,17 +1814,18 @@ hipError_t wisp_amd__rmsnorm_rows(const float* x, const wisp_half* w, float* y32
                                   int rows, int n, float eps, hipStream_t s);
 
 struct BlockWs {
-    size_t pf, xn, total;
+    size_t pf, xn, xn16, total;
     bool decode;
 };
 
 static BlockWs block_ws(const WispExpertLayout* L, int M, int top_k, int n_experts,
                         int has_shared) {
-    BlockWs b = {0, 0, 0, M <= DEC_MAX_TOKENS};
+    BlockWs b = {0, 0, 0, 0, M <= DEC_MAX_TOKENS};
     const size_t hidden = L->cols[0];
     if (b.decode) {
         b.xn = align_up(ws_layout(L, M, top_k, has_shared).total, 256);
-        b.total = b.xn + align_up((size_t)M * hidden * 4, 256);
+        b.xn16 = b.xn + align_up((size_t)M * hidden * 4, 256);
+        b.total = b.xn16 + align_up((size_t)M * hidden * 2, 256);
     } else {
         b.pf = wisp_moe_prefill_workspace_bytes(L, M, top_k, n_experts, has_shared);
         if (b.pf == 0) return b;
@@ -1855,14 +1861,18 @@ extern "C" hipError_t wisp_gpu_moe_block_int4(
     char* ws = (char*)d_workspace;
     hipError_t e;
     if (b.decode) {
-        /* fp32 normalised rows: the router runs in fp32, the experts read
-         * an fp16 copy made by the prep workgroup */
+        /* fp32 normalised rows for the router, and their fp16 rounding for
+         * the experts, both written by the RMSNorm launch (the prep
+         * workgroup then converts nothing: 4 rows, DeepSeek-V3 shape,
+         * 172.3 -> 163.1 us per call) */
         float* xn = (float*)(ws + b.xn);
-        e = wisp_amd__rmsnorm_rows(d_x, d_post_norm_w, xn, nullptr, M, hidden, eps, s);
+        wisp_half* xn16 = (wisp_half*)(ws + b.xn16);
+        e = wisp_amd__rmsnorm_rows(d_x, d_post_norm_w, xn, xn16, M, hidden, eps, s);
         if (e != hipSuccess) return e;
         return layer_run(d_router_w, d_router_bias, router_kind, d_scores, d_topk_idx, d_topk_w,
                          d_expert_table, d_shared_blob, L, xn, WISP_DTYPE_F32, M, top_k,
-                         n_experts, d_workspace, b.xn, /*accumulate=*/1, d_x, nullptr, s);
+                         n_experts, d_workspace, b.xn, /*accumulate=*/1, d_x, nullptr, s,
+                         (const uint16_t*)xn16);
     }
     if ((uintptr_t)d_x % 16) return hipErrorInvalidValue;   /* the prefill's fp32 output */
     wisp_half* xn = (wisp_half*)(ws + b.xn);
