@@ -446,6 +446,13 @@ def measure_prefill(layer, n_tokens, steps, warmup, replays):
     }
 
 
+def _header_int(name):
+    """An integer #define of include/wisp_amd.h."""
+    import re
+    hdr = os.path.join(os.path.dirname(os.path.abspath(__file__)), "include", "wisp_amd.h")
+    return int(re.search(rf"#define {name} (\d+)", open(hdr).read()).group(1))
+
+
 def measure_block(layer, rows, steps, warmup, replays, per_token_us):
     """The MoE block entry (x += MoE(RMSNorm(x) * w_norm), router on the
     normalised rows) on `rows` drafted tokens of one speculative-verify
@@ -513,7 +520,8 @@ def measure_block(layer, rows, steps, warmup, replays, per_token_us):
             "us_per_row": round(us / rows, 3),
             "per_token_loop_us": round(rows * per_token_us, 3),
             "speedup_vs_per_token_loop": round(rows * per_token_us / us, 3),
-            "path": "fused decode (<= 4 rows)" if rows <= 4 else "grouped GEMM (> 4 rows)"}
+            "path": "fused decode, calls of up to 4 rows"
+                    if rows <= _header_int("WISP_BLOCK_DECODE_MAX_ROWS") else "grouped GEMM"}
 
 
 def measure_streaming(n_layers=8, steps=256, slot_frac=0.30, seed=55, n_templates=16):

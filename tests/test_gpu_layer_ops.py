@@ -6,9 +6,10 @@
   oracle on other sizes, aligned and not (the scalar fallbacks).
 * wisp_gpu_moe_block_int4, x += MoE(RMSNorm(x) * w) over n rows of the
   residual stream, against the oracle's composition (rmsnorm, router,
-  run_moe, residual add): 1 and 3 rows (the fused decode, fp32 routing), 4
-  rows as a speculative-verify batch checked against four one-row calls,
-  and 9 and 40 rows (routing on fp16 rows, then the grouped GEMM).
+  run_moe, residual add): 1, 3 and 7 rows (the fused decode, fp32 routing,
+  in calls of up to 4 rows), 4 rows as a speculative-verify batch checked
+  against four one-row calls, and 9 and 40 rows (routing on fp16 rows, then
+  the grouped GEMM).
 
 Bars: fp32 elementwise ops within 1e-6 relative (the GPU sums in fp32, the
 reference's RMSNorm in double); MoE outputs at tests/gpu_util.py's bar."""
@@ -25,6 +26,19 @@ from wisp_amd.hip import DeviceBuffer, synchronize, to_device
 
 pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "layer_ops.npz")
+
+
+def _block_decode_max_rows():
+    """WISP_BLOCK_DECODE_MAX_ROWS as include/wisp_amd.h defines it."""
+    hdr = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                       "wisp_amd.h")
+    import re
+    m = re.search(r"#define WISP_BLOCK_DECODE_MAX_ROWS (\d+)", open(hdr).read())
+    assert m, "WISP_BLOCK_DECODE_MAX_ROWS not found"
+    return int(m.group(1))
+
+
+BLOCK_DECODE_MAX_ROWS = _block_decode_max_rows()
 
 
 def _close(got, want, rel=1e-6, what=""):
@@ -114,7 +128,7 @@ class _Block:
                            idx.ptr, w.ptr, self.arena.table.ptr, self.sh.ptr + 8,
                            self.arena.layout, M, self.top_k, self.n_exp, ws)
         synchronize()
-        if M <= 4:
+        if M <= BLOCK_DECODE_MAX_ROWS:
             assert moe.decode_status(ws) == 0
         return (dx.download(np.float32, x.shape), idx.download(np.int32, (M, self.top_k)),
                 w.download(np.float32, (M, self.top_k)))
@@ -135,14 +149,14 @@ class _Block:
         return x_row + ffn, ffn
 
 
-@pytest.mark.parametrize("M", [1, 3, 9, 40])
+@pytest.mark.parametrize("M", [1, 3, 7, 9, 40])
 def test_moe_block_matches_oracle_composition(M):
     print(f"moe block: {M} rows", flush=True)
     b = _Block(600 + M)
     x = (b.rng.standard_normal((M, b.hidden)) * 1.5).astype(np.float32)
     got, gi, gw = b.run(x)
     for t in range(M):
-        want, ffn = b.want(x[t], M > 4, gi[t], gw[t])
+        want, ffn = b.want(x[t], M > BLOCK_DECODE_MAX_ROWS, gi[t], gw[t])
         assert_close(got[t] - x[t], ffn, f"row {t}: the added ffn")
 
 

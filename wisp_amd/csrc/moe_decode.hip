@@ -1813,6 +1813,11 @@ extern "C" hipError_t wisp_gpu_moe_layer_decode_int4_noalloc(
 hipError_t wisp_amd__rmsnorm_rows(const float* x, const wisp_half* w, float* y32, wisp_half* y16,
                                   int rows, int n, float eps, hipStream_t s);
 
+/* Rows up to which the MoE block runs the fused decode (fp32 routing), in
+ * calls of up to DEC_MAX_TOKENS rows; more rows take the grouped GEMM. */
+#ifndef BLOCK_DECODE_MAX_ROWS
+#define BLOCK_DECODE_MAX_ROWS WISP_BLOCK_DECODE_MAX_ROWS
+#endif
 struct BlockWs {
     size_t pf, xn, xn16, total;
     bool decode;
@@ -1820,10 +1825,11 @@ struct BlockWs {
 
 static BlockWs block_ws(const WispExpertLayout* L, int M, int top_k, int n_experts,
                         int has_shared) {
-    BlockWs b = {0, 0, 0, 0, M <= DEC_MAX_TOKENS};
+    BlockWs b = {0, 0, 0, 0, M <= BLOCK_DECODE_MAX_ROWS};
     const size_t hidden = L->cols[0];
     if (b.decode) {
-        b.xn = align_up(ws_layout(L, M, top_k, has_shared).total, 256);
+        const int mc = M < DEC_MAX_TOKENS ? M : DEC_MAX_TOKENS;   /* rows per decode call */
+        b.xn = align_up(ws_layout(L, mc, top_k, has_shared).total, 256);
         b.xn16 = b.xn + align_up((size_t)M * hidden * 4, 256);
         b.total = b.xn16 + align_up((size_t)M * hidden * 2, 256);
     } else {
@@ -1869,10 +1875,18 @@ extern "C" hipError_t wisp_gpu_moe_block_int4(
         wisp_half* xn16 = (wisp_half*)(ws + b.xn16);
         e = wisp_amd__rmsnorm_rows(d_x, d_post_norm_w, xn, xn16, M, hidden, eps, s);
         if (e != hipSuccess) return e;
-        return layer_run(d_router_w, d_router_bias, router_kind, d_scores, d_topk_idx, d_topk_w,
-                         d_expert_table, d_shared_blob, L, xn, WISP_DTYPE_F32, M, top_k,
-                         n_experts, d_workspace, b.xn, /*accumulate=*/1, d_x, nullptr, s,
-                         (const uint16_t*)xn16);
+        /* up to DEC_MAX_TOKENS rows per decode call, in row order on s */
+        for (int r0 = 0; r0 < M; r0 += DEC_MAX_TOKENS) {
+            const int mc = M - r0 < DEC_MAX_TOKENS ? M - r0 : DEC_MAX_TOKENS;
+            e = layer_run(d_router_w, d_router_bias, router_kind,
+                          d_scores + (size_t)r0 * n_experts, d_topk_idx + (size_t)r0 * top_k,
+                          d_topk_w + (size_t)r0 * top_k, d_expert_table, d_shared_blob, L,
+                          xn + (size_t)r0 * hidden, WISP_DTYPE_F32, mc, top_k, n_experts,
+                          d_workspace, b.xn, /*accumulate=*/1, d_x + (size_t)r0 * hidden,
+                          nullptr, s, (const uint16_t*)(xn16 + (size_t)r0 * hidden));
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
     }
     if ((uintptr_t)d_x % 16) return hipErrorInvalidValue;   /* the prefill's fp32 output */
     wisp_half* xn = (wisp_half*)(ws + b.xn);
