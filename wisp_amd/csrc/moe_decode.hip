@@ -259,6 +259,16 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
                                    __HIP_MEMORY_SCOPE_AGENT);
             }
         }
+        /* after its logits: this workgroup's slice of the fp16 copy of x
+         * that the next launch's gate/up reads (when it cannot read the
+         * caller's x), so the prep workgroup converts nothing */
+        if (P.xconv) {
+            const int n = M * P.hidden;
+            const int chunk = (n + R.n_rwg - 1) / R.n_rwg;
+            const int i1 = min(n, ((int)blockIdx.x + 1) * chunk);
+            for (int i = (int)blockIdx.x * chunk + (int)threadIdx.x; i < i1; i += DEC_PREP_THREADS)
+                P.xconv[i] = __builtin_bit_cast(uint16_t, (f16)xval<XT>(x, i));
+        }
         return;
     }
 
@@ -271,8 +281,9 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     for (int i = threadIdx.x; i < P.max_u * P.upe; i += blockDim.x) P.hcnt[i * DEC_HCNT_STRIDE] = 0;
     if (P.gsplit > 1 && !P.gfinish)   /* arrival counters of the K splits */
         for (int i = threadIdx.x; i < P.max_u * (P.inter / 16); i += blockDim.x) P.gcnt[i] = 0;
-    /* x -> fp16 copy when the gate/up kernel cannot read the caller's x */
-    if (P.xconv) {
+    /* x -> fp16 copy when the gate/up kernel cannot read the caller's x
+     * (with router workgroups in this launch, they make it) */
+    if (P.xconv && R.mode != 3) {
         for (int i = threadIdx.x; i < M * P.hidden; i += blockDim.x)
             P.xconv[i] = __builtin_bit_cast(uint16_t, (f16)xval<XT>(x, i));
     }
