@@ -259,10 +259,11 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
                                    __HIP_MEMORY_SCOPE_AGENT);
             }
         }
-        /* after its logits: this workgroup's slice of the fp16 copy of x
-         * that the next launch's gate/up reads (when it cannot read the
-         * caller's x), so the prep workgroup converts nothing */
-        if (P.xconv) {
+        /* fp32 x, after its logits: this workgroup's slice of the fp16 copy
+         * of x that the next launch's gate/up reads, so the prep workgroup
+         * converts nothing (the fp16 instantiation, whose copy is only
+         * needed for an unaligned x, leaves it to the prep workgroup) */
+        if constexpr (sizeof(XT) == 4) if (P.xconv) {
             const int n = M * P.hidden;
             const int chunk = (n + R.n_rwg - 1) / R.n_rwg;
             const int i1 = min(n, ((int)blockIdx.x + 1) * chunk);
@@ -282,8 +283,8 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     if (P.gsplit > 1 && !P.gfinish)   /* arrival counters of the K splits */
         for (int i = threadIdx.x; i < P.max_u * (P.inter / 16); i += blockDim.x) P.gcnt[i] = 0;
     /* x -> fp16 copy when the gate/up kernel cannot read the caller's x
-     * (with router workgroups in this launch, they make it) */
-    if (P.xconv && R.mode != 3) {
+     * (for fp32 x with router workgroups in this launch, they make it) */
+    if (P.xconv && (R.mode != 3 || sizeof(XT) == 2)) {
         for (int i = threadIdx.x; i < M * P.hidden; i += blockDim.x)
             P.xconv[i] = __builtin_bit_cast(uint16_t, (f16)xval<XT>(x, i));
     }
