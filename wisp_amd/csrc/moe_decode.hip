@@ -1256,6 +1256,8 @@ void down_kernel(const DecodeParams P) {
      * zero scale), the row tile's scales, then its weights. */
     uint16_t* xs = (uint16_t*)(smem + L.x_off);
     const uint16_t* hsrc = P.hperm + (size_t)u * K + lb0 * 128;
+    static_assert(DEC_UNIT_BLOCKS * 128 * 2 == 2 * 1024,
+                  "a unit's h' per token is staged as two 1 KB pieces");
     constexpr int PCS = (2 * M + DN_WAVES - 1) / DN_WAVES;
 #pragma unroll
     for (int k = 0; k < PCS; k++) {
