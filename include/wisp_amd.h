@@ -346,7 +346,9 @@ hipError_t wisp_gpu_moe_layer_decode_int4_noalloc(
  * Needs hidden % 256 == 0 and a 16-byte aligned x for more than 4 rows.
  * The workspace (wisp_moe_block_workspace_bytes for the largest n_tokens
  * used) is dedicated to this call and may be shared by calls of different
- * n_tokens, one at a time; it needs no zeroing. */
+ * n_tokens, one at a time; it needs no zeroing. Up to
+ * WISP_BLOCK_DECODE_MAX_ROWS rows, wisp_moe_decode_status on it reports the
+ * bounded waits of every decode call the block made. */
 /* DeepSeek-V3 shape, per call: 8 rows 325 us in two decode calls against
  * 367 us in the grouped GEMM; 12 rows 481 against 470 us. */
 #define WISP_BLOCK_DECODE_MAX_ROWS 8

@@ -91,6 +91,7 @@ struct DecodeParams {
     uint32_t* status;     /* DEC_STATUS_* bits of this call's bounded waits that gave up */
     int poll_limit;       /* polls of one hand-off word or counter before giving up */
     int poll_extra;       /* added to every wait target: nonzero only to force a give-up */
+    int keep_status;      /* 1: keep the status bits of the calls before (one MoE block) */
 };
 
 /* Routing inputs of the prep kernel. mode 0: idx/w are given; mode 1: raw
@@ -274,8 +275,9 @@ __global__ __launch_bounds__(DEC_PREP_THREADS) void decode_prep_kernel(
     }
 
     /* this call's status starts clear (the down waits of the next launch
-     * and the routing wait below set bits) */
-    if (threadIdx.x == 0)
+     * and the routing wait below set bits), unless it continues the calls
+     * of one MoE block */
+    if (threadIdx.x == 0 && !P.keep_status)
         __hip_atomic_store(P.status, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (int e = threadIdx.x; e < n_experts; e += blockDim.x) s_tab[e] = (const uint8_t*)table[e];
     for (int i = threadIdx.x; i < P.hidden / 16; i += blockDim.x) P.tile_cnt[i] = 0;
@@ -1578,7 +1580,7 @@ static hipError_t decode_run(const void* const* d_expert_table, const void* d_sh
                              RouteArgs R, int top_k, int n_experts, void* d_workspace,
                              size_t workspace_bytes, int accumulate, float* d_out_f32,
                              wisp_half* d_out_f16, hipStream_t s,
-                             const uint16_t* x16 = nullptr) {
+                             const uint16_t* x16 = nullptr, bool keep_status = false) {
     if (wisp_expert_layout_check(L) != hipSuccess) return hipErrorInvalidValue;
     const WsLayout w = ws_layout(L, M, top_k, d_shared_blob != nullptr);
     if (workspace_bytes < w.total) return hipErrorInvalidValue;
@@ -1627,6 +1629,7 @@ static hipError_t decode_run(const void* const* d_expert_table, const void* d_sh
     P.status = (uint32_t*)(ws + DEC_STATUS_OFFSET);
     P.poll_limit = g_poll_limit;
     P.poll_extra = g_poll_extra;
+    P.keep_status = keep_status ? 1 : 0;
 
     const size_t lds = prep_lds_bytes(R.mode, n_experts, M);
     int grid = 1;
@@ -1710,7 +1713,8 @@ static hipError_t layer_run(const wisp_half* d_router_w, const wisp_half* d_rout
                             const WispExpertLayout* L, const void* d_x, int x_dtype, int n_tokens,
                             int top_k, int n_experts, void* d_workspace, size_t workspace_bytes,
                             int accumulate, float* d_out_f32, wisp_half* d_out_f16,
-                            hipStream_t s, const uint16_t* x16 = nullptr) {
+                            hipStream_t s, const uint16_t* x16 = nullptr,
+                            bool keep_status = false) {
     const int hidden = (int)L->cols[0];
     /* the router GEMV runs in router workgroups of the prep launch (mode 3):
      * each thread takes at most 2 16-byte pieces of a row, so rows up to
@@ -1732,7 +1736,7 @@ static hipError_t layer_run(const wisp_half* d_router_w, const wisp_half* d_rout
     }
     return decode_run(d_expert_table, d_shared_blob, L, d_x, x_dtype, n_tokens, R, top_k,
                       n_experts, d_workspace, workspace_bytes, accumulate, d_out_f32, d_out_f16, s,
-                      x16);
+                      x16, keep_status);
 }
 
 extern "C" hipError_t wisp_gpu_moe_layer_decode_int4(
@@ -1897,7 +1901,8 @@ extern "C" hipError_t wisp_gpu_moe_block_int4(
                           d_topk_w + (size_t)r0 * top_k, d_expert_table, d_shared_blob, L,
                           xn + (size_t)r0 * hidden, WISP_DTYPE_F32, mc, top_k, n_experts,
                           d_workspace, b.xn, /*accumulate=*/1, d_x + (size_t)r0 * hidden,
-                          nullptr, s, (const uint16_t*)(xn16 + (size_t)r0 * hidden));
+                          nullptr, s, (const uint16_t*)(xn16 + (size_t)r0 * hidden),
+                          /*keep_status=*/r0 > 0);
             if (e != hipSuccess) return e;
         }
         return hipSuccess;
