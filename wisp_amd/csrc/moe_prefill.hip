@@ -52,6 +52,7 @@
 #define PF_WIDE_RING 2         /* weight blocks in the ring of the wide full-tile kernel */
 #define PF_SMALL_CHUNK_DN 16      /* down K chunk of the <= 64-token tiles (all 16 blocks of inter 2048) */
 #define PF_CHUNK 8                /* K blocks per straight-line pipeline chunk (when they divide K) */
+#define PF_COMBINE_SLOTS 16       /* slots per token the combine loads at once (top_k + shared) */
 #define PF_WIDE_CHUNK_DN 16       /* down K chunk of the wide full-tile kernel (all 16 blocks of inter 2048) */
 
 struct PfParams {
@@ -608,12 +609,31 @@ __global__ __launch_bounds__(256) void pf_combine_kernel(const PfParams P) {
     if (i >= (size_t)P.n_tokens * c8) return;
     const int t = (int)(i / c8), c = 8 * (int)(i - (size_t)t * c8);
     float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int k = 0; k < P.top_k1; k++) {
-        const int p = P.inv[t * P.top_k1 + k];
-        if (p >= 0) {
-            const h8 v = *(const h8*)(P.Y + (size_t)p * P.hidden + c);
+    if (P.top_k1 <= PF_COMBINE_SLOTS) {
+        /* every slot's position, then every row, then the sum in slot
+         * order: two round trips instead of two per slot */
+        int pv[PF_COMBINE_SLOTS];
 #pragma unroll
-            for (int q = 0; q < 8; q++) y[q] += (float)v[q];
+        for (int k = 0; k < PF_COMBINE_SLOTS; k++)
+            pv[k] = k < P.top_k1 ? P.inv[t * P.top_k1 + k] : -1;
+        h8 v[PF_COMBINE_SLOTS];
+#pragma unroll
+        for (int k = 0; k < PF_COMBINE_SLOTS; k++)
+            v[k] = pv[k] >= 0 ? *(const h8*)(P.Y + (size_t)pv[k] * P.hidden + c) : (h8){};
+#pragma unroll
+        for (int k = 0; k < PF_COMBINE_SLOTS; k++)
+            if (pv[k] >= 0) {
+#pragma unroll
+                for (int q = 0; q < 8; q++) y[q] += (float)v[k][q];
+            }
+    } else {
+        for (int k = 0; k < P.top_k1; k++) {
+            const int p = P.inv[t * P.top_k1 + k];
+            if (p >= 0) {
+                const h8 v = *(const h8*)(P.Y + (size_t)p * P.hidden + c);
+#pragma unroll
+                for (int q = 0; q < 8; q++) y[q] += (float)v[q];
+            }
         }
     }
     const size_t o = (size_t)t * P.hidden + c;
