@@ -450,7 +450,8 @@ def _header_int(name):
     """An integer #define of include/wisp_amd.h."""
     import re
     hdr = os.path.join(os.path.dirname(os.path.abspath(__file__)), "include", "wisp_amd.h")
-    return int(re.search(rf"#define {name} (\d+)", open(hdr).read()).group(1))
+    with open(hdr) as f:
+        return int(re.search(rf"#define {name} (\d+)", f.read()).group(1))
 
 
 def measure_block(layer, rows, steps, warmup, replays, per_token_us):

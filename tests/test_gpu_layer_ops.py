@@ -33,7 +33,8 @@ def _block_decode_max_rows():
     hdr = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
                        "wisp_amd.h")
     import re
-    m = re.search(r"#define WISP_BLOCK_DECODE_MAX_ROWS (\d+)", open(hdr).read())
+    with open(hdr) as f:
+        m = re.search(r"#define WISP_BLOCK_DECODE_MAX_ROWS (\d+)", f.read())
     assert m, "WISP_BLOCK_DECODE_MAX_ROWS not found"
     return int(m.group(1))
 
